@@ -1,0 +1,30 @@
+// ABI bookkeeping: version and the per-thread last-error string.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "gdn_common.h"
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+int gdn_set_error(int code, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int gdn_check_launch(const char *what)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return gdn_set_error(GDN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return GDN_OK;
+}
+
+extern "C" int gdn_abi_version(void) { return GDN_HIP_ABI_VERSION; }
+
+extern "C" const char *gdn_last_error(void) { return g_last_error; }

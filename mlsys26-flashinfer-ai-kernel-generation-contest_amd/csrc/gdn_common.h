@@ -1,0 +1,70 @@
+// Shared device helpers for the gfx950 Gated DeltaNet kernels: bf16 conversion,
+// wavefront reductions on DPP, vector types, and the host-side error channel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gdn_hip.h"
+
+namespace gdn {
+
+typedef uint16_t bf16_t;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h)
+{
+    return __uint_as_float(h << 16);
+}
+
+// Low / high bf16 of a packed pair -> float (exact).
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u)
+        return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// DPP control words (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <- lane 7-i within each 8 lanes
+constexpr int kDppRowMirror = 0x140;      // lane i <- lane 15-i within each 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over each aligned group of 8 lanes; every lane of the group receives the
+// same bits (the adds pair operands symmetrically).
+__device__ __forceinline__ float group8_sum(float x)
+{
+    x += dpp_mov<kDppRowHalfMirror>(x);
+    x += dpp_mov<kDppQuadXor1>(x);
+    x += dpp_mov<kDppQuadXor2>(x);
+    return x;
+}
+
+// Sum over each aligned group of 16 lanes.
+__device__ __forceinline__ float group16_sum(float x)
+{
+    x += dpp_mov<kDppRowMirror>(x);
+    return group8_sum(x);
+}
+
+}  // namespace gdn
+
+// Host-side error channel (gdn_abi.hip).
+int gdn_set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int gdn_check_launch(const char *what);
