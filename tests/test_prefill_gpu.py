@@ -1,0 +1,175 @@
+"""GPU parity of gdn_prefill (HIP, chunked WY form) against the float64 CPU oracle.
+
+Tolerances (as applied here): output bf16 atol = rtol = 2e-2; new_state fp32
+rtol = 1e-3 with atol = 1e-4; both-condition rule of FAQ.md:104-110.
+"""
+import pytest
+import torch
+
+from gdn_hip import gdn_decode, gdn_prefill
+from gdn_hip.inputs import prefill_inputs, varlen_lengths
+from gdn_hip.parity import check_output, check_state
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(inp):
+    return O.prefill(inp.q, inp.k, inp.v, inp.state, inp.A_log, inp.a, inp.dt_bias, inp.b,
+                     inp.cu_seqlens, inp.scale)
+
+
+def _check(out, ns, ref_out, ref_ns, label):
+    vo = check_output(out, ref_out)
+    vs = check_state(ns, ref_ns)
+    print(f"[{label}] output {vo} | state {vs}", flush=True)
+    assert vo.ok, f"{label}: output {vo}"
+    assert vs.ok, f"{label}: new_state {vs}"
+
+
+def _run(dev, inp, label, **kw):
+    print(f"[{label}] launching T={inp.q.shape[0]} lens={inp.seqlens[:8]}...", flush=True)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out, ns = gdn_prefill(*g.args(), **kw)
+    torch.cuda.synchronize()
+    _check(out, ns, ref_out, ref_ns, label)
+    return g, out, ns
+
+
+@pytest.mark.parametrize("lens", [[1], [5], [63], [64], [65], [128], [129], [200, 37]])
+def test_prefill_small(dev, lens):
+    _run(dev, prefill_inputs(lens, seed=len(lens) * 100 + lens[0], with_state=True),
+         f"lens={lens}")
+
+
+def test_prefill_single_4k_zero_state(dev):
+    """One 4096-token sequence, zero initial state (state=None)."""
+    _run(dev, prefill_inputs([4096], seed=3, with_state=False), "4k state=None")
+
+
+def test_prefill_varlen_16(dev):
+    """16 sequences, lengths ~U[64,1024] from the seed, non-zero fp32 initial state."""
+    lens = varlen_lengths(16, seed=0)
+    _run(dev, prefill_inputs(lens, seed=0, with_state=True), "varlen16")
+
+
+@pytest.mark.parametrize("gates", ["mild", "none"])
+def test_prefill_long_memory_gates(dev, gates):
+    """alpha ~ 0.99 or exactly 1: the state carries across many chunks."""
+    _run(dev, prefill_inputs([300, 700, 64], seed=5, with_state=True, gates=gates,
+                             state_std=0.1), f"gates={gates}")
+
+
+@pytest.mark.parametrize("hqk,hv", [(4, 8), (8, 8), (2, 8), (1, 4)])
+def test_prefill_head_layouts(dev, hqk, hv):
+    _run(dev, prefill_inputs([150, 90, 257], hqk=hqk, hv=hv, seed=9, with_state=True),
+         f"hqk={hqk} hv={hv}")
+
+
+def test_prefill_empty_sequences_and_gaps(dev):
+    """Zero-length sequences keep their state; tokens outside every sequence read as
+    zero output (gdn_prefill/solution/triton/kernel.py:286)."""
+    _run(dev, prefill_inputs([0, 70, 0, 0, 130, 0], seed=17, with_state=True, pad_tokens=45),
+         "empty+gaps")
+
+
+def test_prefill_int64_cu_seqlens(dev):
+    _run(dev, prefill_inputs([99, 1, 250], seed=19, with_state=True, cu_dtype=torch.int64),
+         "cu int64")
+
+
+def test_prefill_inplace_state(dev):
+    inp = prefill_inputs([180, 75], seed=23, with_state=True)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out, ns = gdn_prefill(*g.args(), new_state=g.state)
+    torch.cuda.synchronize()
+    assert ns.data_ptr() == g.state.data_ptr()
+    _check(out, ns, ref_out, ref_ns, "in-place")
+
+
+def test_prefill_explicit_zero_state_equals_none(dev):
+    inp = prefill_inputs([333], seed=29, with_state=False).to(dev)
+    o1, s1 = gdn_prefill(*inp.args())
+    z = torch.zeros((1, 32, 128, 128), dtype=torch.float32, device=dev)
+    args = list(inp.args())
+    args[3] = z
+    o2, s2 = gdn_prefill(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+def test_prefill_strided_and_preallocated(dev):
+    """q/k/v as views of a fused projection; preallocated (poisoned) outputs."""
+    inp = prefill_inputs([77, 160], seed=31, with_state=True)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    T = g.q.shape[0]
+    qkv = torch.empty((T, 16 + 16 + 32, 128), dtype=torch.bfloat16, device=dev)
+    qkv[:, :16], qkv[:, 16:32], qkv[:, 32:] = g.q, g.k, g.v
+    out = torch.full((T, 32, 128), 7.0, dtype=torch.bfloat16, device=dev)
+    ns = torch.full_like(g.state, 7.0)
+    o, s = gdn_prefill(qkv[:, :16], qkv[:, 16:32], qkv[:, 32:], g.state, g.A_log, g.a,
+                       g.dt_bias, g.b, g.cu_seqlens, g.scale, output=out, new_state=ns)
+    torch.cuda.synchronize()
+    assert o.data_ptr() == out.data_ptr() and s.data_ptr() == ns.data_ptr()
+    _check(o, s, ref_out, ref_ns, "strided")
+
+
+def test_prefill_deterministic(dev):
+    inp = prefill_inputs(varlen_lengths(8, seed=4), seed=4, with_state=True).to(dev)
+    o1, s1 = gdn_prefill(*inp.args())
+    o2, s2 = gdn_prefill(*inp.args())
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+def test_prefill_no_sequences_and_no_tokens(dev):
+    inp = prefill_inputs([], seed=1, with_state=True, pad_tokens=10).to(dev)
+    out, ns = gdn_prefill(*inp.args())
+    torch.cuda.synchronize()
+    assert out.shape == (10, 32, 128) and torch.all(out == 0)
+    assert ns.shape == (0, 32, 128, 128)
+    inp = prefill_inputs([0, 0], seed=2, with_state=True).to(dev)
+    out, ns = gdn_prefill(*inp.args())
+    torch.cuda.synchronize()
+    assert out.shape == (0, 32, 128) and torch.equal(ns, inp.state)
+
+
+def test_prefill_resume_split(dev):
+    """prefill(x[:m]) then prefill(x[m:], state) matches prefill(x) (state handoff)."""
+    inp = prefill_inputs([500], seed=37, with_state=True, gates="mild").to(dev)
+    full_o, full_s = gdn_prefill(*inp.args())
+    m = 203
+    cu1 = torch.tensor([0, m], dtype=torch.int32, device=dev)
+    cu2 = torch.tensor([0, 500 - m], dtype=torch.int32, device=dev)
+    o1, s1 = gdn_prefill(inp.q[:m], inp.k[:m], inp.v[:m], inp.state, inp.A_log, inp.a[:m],
+                         inp.dt_bias, inp.b[:m], cu1, inp.scale)
+    o2, s2 = gdn_prefill(inp.q[m:], inp.k[m:], inp.v[m:], s1, inp.A_log, inp.a[m:],
+                         inp.dt_bias, inp.b[m:], cu2, inp.scale)
+    torch.cuda.synchronize()
+    vo = check_output(torch.cat([o1, o2]), full_o)
+    vs = check_state(s2, full_s)
+    print(f"[resume] output {vo} | state {vs}", flush=True)
+    assert vo.ok and vs.ok
+
+
+def test_prefill_then_decode_matches_longer_prefill(dev):
+    """Prefill's new_state feeds decode (same k-last layout): prefill(x) then decode(t)
+    equals prefill(x || t) in the last token's output and the final state."""
+    L = 257
+    inp = prefill_inputs([L + 1], seed=41, with_state=True).to(dev)
+    full_o, full_s = gdn_prefill(*inp.args())
+    cu = torch.tensor([0, L], dtype=torch.int32, device=dev)
+    _, s = gdn_prefill(inp.q[:L], inp.k[:L], inp.v[:L], inp.state, inp.A_log, inp.a[:L],
+                       inp.dt_bias, inp.b[:L], cu, inp.scale)
+    t = slice(L, L + 1)
+    od, sd = gdn_decode(inp.q[t].unsqueeze(0), inp.k[t].unsqueeze(0), inp.v[t].unsqueeze(0),
+                        s, inp.A_log, inp.a[t].unsqueeze(0), inp.dt_bias, inp.b[t].unsqueeze(0),
+                        inp.scale)
+    torch.cuda.synchronize()
+    vo = check_output(od[0, 0], full_o[L])
+    vs = check_state(sd, full_s)
+    print(f"[prefill->decode] output {vo} | state {vs}", flush=True)
+    assert vo.ok and vs.ok
