@@ -155,6 +155,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all",
+                    help="run one path only (profiling runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also launch a plain 256 MiB device copy (rocprof counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this path runs on one GPU "
@@ -169,9 +173,24 @@ def main():
     from gdn_hip import _lib
 
     _lib.load()
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 268435456-byte device copies")
+        del src, dst
+    if args.only == "prefill":
+        pre = bench_prefill(max(3, min(args.steps, 50)), 2)
+        log(f"prefill: T={pre['tokens']} {pre['ms'] * 1e3:.1f} us/step "
+            f"{pre['mtok_s']:.1f} Mtok/s {pre['tflops']:.1f} TFLOP/s")
+        return
     log(f"decode B=64: warmup {args.warmup}, steps {args.steps}")
     dec = bench_decode(args.steps, args.warmup)
     log(f"decode: {dec['ms'] * 1e3:.2f} us/step, {dec['gbs']:.0f} GB/s (trials {dec['trials']})")
+    if args.only == "decode":
+        return
     pre = None
     if not args.no_prefill:
         psteps = max(3, min(args.steps, 50))

@@ -94,9 +94,10 @@ def _stream(dev):
 def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state):
     """Validate like the reference host wrapper and build the ABI params.
 
-    Returns (params, output, new_state, copy_back) where copy_back lists
+    Returns (params, output, new_state, copy_back, keep): copy_back lists
     (user_tensor, kernel_tensor) pairs to copy after the launch (only when a user
-    buffer's layout is not one the kernel writes directly)."""
+    buffer's layout is not one the kernel writes directly); keep holds every tensor
+    the params point at, so they outlive the launch."""
     _need_tensor("q", q, torch.bfloat16, 4)
     B, T, HQK, D = q.shape
     _need_tensor("k", k, torch.bfloat16, 4)
@@ -122,6 +123,12 @@ def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_sta
     _need_shape("dt_bias", dt_bias, (HV,))
     _need_tensor("b", b, torch.bfloat16, 3)
     _need_shape("b", b, (B, T, HV))
+    if output is not None:
+        _need_tensor("output", output, torch.bfloat16, 4)
+        _need_shape("output", output, (B, T, HV, D))
+    if new_state is not None:
+        _need_tensor("new_state", new_state, torch.float32, 4)
+        _need_shape("new_state", new_state, (B, HV, D, D))
     dev = q.device
     _need_device(dev, k=k, v=v, state=state, A_log=A_log, a=a, dt_bias=dt_bias, b=b,
                  output=output, new_state=new_state)
@@ -131,14 +138,8 @@ def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_sta
     # the kernel skips the read)
     if output is None:
         output = torch.empty((B, T, HV, D), dtype=torch.bfloat16, device=dev)
-    else:
-        _need_tensor("output", output, torch.bfloat16, 4)
-        _need_shape("output", output, (B, T, HV, D))
     if new_state is None:
         new_state = torch.empty((B, HV, D, D), dtype=torch.float32, device=dev)
-    else:
-        _need_tensor("new_state", new_state, torch.float32, 4)
-        _need_shape("new_state", new_state, (B, HV, D, D))
 
     qk_ok = (8, 4)
     st_ok = (16, 4)
@@ -290,22 +291,22 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=
     _need_shape("dt_bias", dt_bias, (HV,))
     _need_tensor("b", b, torch.bfloat16, 2)
     _need_shape("b", b, (T, HV))
+    HO = max(HQK, HV)  # output heads: gdn_prefill/solution/triton/kernel.py:267,283
+    if output is not None:
+        _need_tensor("output", output, torch.bfloat16, 3)
+        _need_shape("output", output, (T, HO, D))
+    if new_state is not None:
+        _need_tensor("new_state", new_state, torch.float32, 4)
+        _need_shape("new_state", new_state, (N, HV, D, D))
     dev = q.device
     _need_device(dev, k=k, v=v, state=state, A_log=A_log, a=a, dt_bias=dt_bias, b=b,
                  cu_seqlens=cu_seqlens, output=output, new_state=new_state)
     scale = _resolve_scale(scale, D)
-    HO = max(HQK, HV)  # output heads: gdn_prefill/solution/triton/kernel.py:267,283
 
     if output is None:
         output = torch.empty((T, HO, D), dtype=torch.bfloat16, device=dev)
-    else:
-        _need_tensor("output", output, torch.bfloat16, 3)
-        _need_shape("output", output, (T, HO, D))
     if new_state is None:
         new_state = torch.empty((N, HV, D, D), dtype=torch.float32, device=dev)
-    else:
-        _need_tensor("new_state", new_state, torch.float32, 4)
-        _need_shape("new_state", new_state, (N, HV, D, D))
     if N == 0 or T == 0:
         # gdn_prefill/solution/triton/kernel.py:286-302: zeroed output, state copied
         output.zero_()

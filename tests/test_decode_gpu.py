@@ -148,3 +148,25 @@ def test_decode_loaded_native_library():
     assert "libgdn_hip.so" in maps
     hip = {ln.split()[-1] for ln in maps.splitlines() if "libamdhip64" in ln}
     assert len(hip) == 1, hip
+
+
+def test_decode_matches_exact_fixture(dev):
+    """HIP decode of the fixture's single-token sequence vs its rational known answer."""
+    import os
+
+    import numpy as np
+
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "gdn_kat_d128.npz"))
+    t = int(f["cu_seqlens"][1])  # second sequence: exactly one token
+
+    def bf(x):
+        return torch.from_numpy(np.ascontiguousarray(x).view(np.int16).copy()).view(
+            torch.bfloat16).to(dev)
+
+    out, ns = gdn_decode(bf(f["q"][t:t + 1][None]), bf(f["k"][t:t + 1][None]),
+                         bf(f["v"][t:t + 1][None]), torch.from_numpy(f["state"][1:2]).to(dev),
+                         torch.from_numpy(f["A_log"]).to(dev), bf(f["a"][t:t + 1][None]),
+                         torch.from_numpy(f["dt_bias"]).to(dev), bf(f["b"][t:t + 1][None]),
+                         float(f["scale"]))
+    torch.cuda.synchronize()
+    _check(out[0, 0], ns[0], f["out"][t], f["new_state"][1], "exact fixture")

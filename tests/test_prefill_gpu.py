@@ -173,3 +173,22 @@ def test_prefill_then_decode_matches_longer_prefill(dev):
     vs = check_state(sd, full_s)
     print(f"[prefill->decode] output {vo} | state {vs}", flush=True)
     assert vo.ok and vs.ok
+
+
+def test_prefill_matches_exact_fixture(dev):
+    """HIP prefill vs the rational-arithmetic known answers (tests/golden/make_golden.py)."""
+    import os
+
+    import numpy as np
+
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "gdn_kat_d128.npz"))
+
+    def bf(x):
+        return torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16).to(dev)
+
+    out, ns = gdn_prefill(bf(f["q"]), bf(f["k"]), bf(f["v"]), torch.from_numpy(f["state"]).to(dev),
+                          torch.from_numpy(f["A_log"]).to(dev), bf(f["a"]),
+                          torch.from_numpy(f["dt_bias"]).to(dev), bf(f["b"]),
+                          torch.from_numpy(f["cu_seqlens"]).to(dev), float(f["scale"]))
+    torch.cuda.synchronize()
+    _check(out, ns, f["out"], f["new_state"], "exact fixture")
