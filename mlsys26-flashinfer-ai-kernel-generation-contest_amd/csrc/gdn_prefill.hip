@@ -40,24 +40,38 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c)
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// hi = bf16(x), lo = bf16(x - hi)
-__device__ __forceinline__ void split_bf16(float x, uint32_t &hi, uint32_t &lo)
-{
-    hi = f32_to_bf16(x);
-    lo = f32_to_bf16(x - bf16_to_f32(hi));
-}
-
 constexpr int kC = 64;   // chunk length
 constexpr int kDK = 128; // head size
 constexpr int kLdK = 136; // padded LDS row (bf16) for 64 x 128 tiles
 constexpr int kLdT = 72;  // padded LDS row (bf16) for 16 x 64 tiles
 
-// Per (chunk, v-head) record in the workspace.
-constexpr int kRecThi = 0;       // bf16 [64][64]  T = (I + A)^-1, high half
-constexpr int kRecTlo = 8192;    // bf16 [64][64]  low half
-constexpr int kRecP = 16384;     // bf16 [64][64]  P (decayed, causal Q K^T)
-constexpr int kRecGates = 24576; // f32 beta[64], gamma[64], dec[64], gammaC
-constexpr int kRecBytes = 25600;
+// Per (chunk, v-head) record in the workspace. 64x64 lower-triangular matrices are
+// stored as their 10 lower 16x16 blocks, block (i, j <= i) at index i(i+1)/2 + j,
+// each block row-major: exactly the rows and 8-column runs an MFMA A operand reads.
+constexpr int kBlk = 256;        // elements per 16x16 block
+constexpr int kRecThi = 0;       // bf16 [10][16][16]  T = (I + A)^-1, high half
+constexpr int kRecTlo = 5120;    // bf16 [10][16][16]  low half
+constexpr int kRecP = 10240;     // bf16 [10][16][16]  P (decayed, causal Q K^T)
+constexpr int kRecGates = 15360; // f32 beta[64], gamma[64], dec[64], gammaC
+constexpr int kRecZero = 16256;  // 16 zero bytes (after the gates): what absent blocks read
+constexpr int kRecBytes = 16384;
+
+__device__ __forceinline__ int tri_blk(int i, int j) { return i * (i + 1) / 2 + j; }
+
+// Workgroup barrier that orders LDS only: global loads issued before it (the next
+// chunk's prefetch) stay in flight across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int K>
+__device__ __forceinline__ float quad_bcast(float x)
+{
+    return dpp_mov<K | (K << 2) | (K << 4) | (K << 6)>(x);
+}
 
 __device__ __forceinline__ int64_t load_cu(const void *cu, int cu64, int i)
 {
@@ -173,27 +187,52 @@ struct PrepArgs {
     int64_t q_st, q_sh, k_st, k_sh, a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
     const int32_t *header, *chunk_tok0, *chunk_len;
     char *records;
-    int HV, ratio;
+    int HQK, HV, ratio;
 };
+
+// Lower-triangular 16x16 tile t of a 64x64 matrix -> (row block, column block).
+__device__ __forceinline__ int tile_i(int t) { return t < 1 ? 0 : (t < 3 ? 1 : (t < 6 ? 2 : 3)); }
+__device__ __forceinline__ int tile_j(int t) { return t - tri_blk(tile_i(t), 0); }
+
+__device__ __forceinline__ float quad_bcast_sel(float x, int k)
+{
+    switch (k & 3) {
+    case 0: return quad_bcast<0>(x);
+    case 1: return quad_bcast<1>(x);
+    case 2: return quad_bcast<2>(x);
+    default: return quad_bcast<3>(x);
+    }
+}
 
 __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
 {
-    const int c = blockIdx.x;
-    const int g = blockIdx.y;
+    // One workgroup per (chunk, v-head). The `ratio` v-heads of one (chunk, q/k head)
+    // read the same K and Q: their workgroups land on one XCD (ids are dealt to the 8
+    // XCDs round-robin), so the second read hits that XCD's L2.
+    const int pid = blockIdx.x, xcd = pid & 7, slot = pid >> 3;
+    const int hh = slot % p.ratio;
+    const int grp = (slot / p.ratio) * 8 + xcd;
+    const int c = grp / p.HQK, g = grp % p.HQK;
     if (c >= p.header[0])
         return;
+    const int h = g * p.ratio + hh;
     const int tok0 = p.chunk_tok0[c];
     const int len = p.chunk_len[c];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
 
-    __shared__ __align__(16) bf16_t Ks[kC][kLdK];
-    __shared__ __align__(16) bf16_t Qs[kC][kLdK];
-    __shared__ __align__(16) float As[kC][kC + 4];
-    __shared__ __align__(16) float Ts[kC][kC + 4];
+    // K and Q (bf16) first; the same bytes then hold A and T (fp32).
+    __shared__ __align__(16) char smem[2 * kC * kLdK * 2];
+    __shared__ __align__(16) bf16_t Ps[10 * kBlk];
     __shared__ __align__(16) float Ms[4][16][17];
     __shared__ float Lg[kC], Bt[kC];
+    bf16_t(*Ks)[kLdK] = (bf16_t(*)[kLdK])smem;
+    bf16_t(*Qs)[kLdK] = (bf16_t(*)[kLdK])(smem + kC * kLdK * 2);
+    float(*As)[kC + 4] = (float(*)[kC + 4])smem;
+    float(*Ts)[kC + 4] = (float(*)[kC + 4])(smem + kC * (kC + 4) * 4);
+    static_assert(2 * kC * (kC + 4) * 4 == 2 * kC * kLdK * 2, "A/T alias K/Q exactly");
 
-    // K, Q chunk rows -> LDS (zero rows past the chunk's length).
+    char *rec = p.records + ((int64_t)c * p.HV + h) * kRecBytes;
+
     for (int s = tid; s < kC * (kDK / 8); s += 256) {
         const int row = s >> 4, col = (s & 15) * 8;
         u32x4 kv = {0u, 0u, 0u, 0u}, qv = {0u, 0u, 0u, 0u};
@@ -204,163 +243,148 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
         *(u32x4 *)&Ks[row][col] = kv;
         *(u32x4 *)&Qs[row][col] = qv;
     }
-    __syncthreads();
 
-    // Row block w of K K^T and Q K^T (only tiles on or below the diagonal).
-    f32x4 kk[4], qk[4];
+    // Gates and in-chunk cumulative log decay: wave 0, one lane per token
+    // (gdn_decode/solution/triton/kernel.py:128-131). Padding tokens: alpha = 1, beta = 0.
+    if (w == 0) {
+        float la = 0.f, bt = 0.f;
+        if (l < len) {
+            const float A_log = p.A_log[h * p.A_log_s];
+            const float dtb = p.dt_bias[h * p.dt_s];
+            const float x = bf16_to_f32(p.a[(int64_t)(tok0 + l) * p.a_st + h * p.a_sh]) + dtb;
+            const float sp = x > 20.f ? x : logf(1.f + expf(x));
+            la = -expf(A_log) * sp;
+            const float bv = bf16_to_f32(p.b[(int64_t)(tok0 + l) * p.b_st + h * p.b_sh]);
+            bt = 1.f / (1.f + expf(-bv));
+        }
+        float L = la;
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        kk[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        qk[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (jt <= w) {
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(L, off, 64);
+            if (l >= off)
+                L += y;
+        }
+        const float Lend = __shfl(L, 63, 64);
+        Lg[l] = L;
+        Bt[l] = bt;
+        float *gates = (float *)(rec + kRecGates);
+        gates[l] = bt;
+        gates[64 + l] = expf(L);
+        gates[128 + l] = expf(Lend - L);
+        if (l == 0)
+            gates[192] = expf(Lend);
+        if (l < 4)
+            ((float *)(rec + kRecZero))[l] = 0.f;
+    }
+    lds_barrier();
+
+    // 20 tile jobs (10 lower tiles of K K^T, 10 of Q K^T), 5 per wave.
+    f32x4 acc[5];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const u32x4 ak = *(const u32x4 *)&Ks[16 * w + lr][ks * 32 + 8 * lg];
-                const u32x4 aq = *(const u32x4 *)&Qs[16 * w + lr][ks * 32 + 8 * lg];
-                const u32x4 bk = *(const u32x4 *)&Ks[16 * jt + lr][ks * 32 + 8 * lg];
-                kk[jt] = mfma_bf16(ak, bk, kk[jt]);
-                qk[jt] = mfma_bf16(aq, bk, qk[jt]);
+    for (int m = 0; m < 5; ++m) {
+        const int job = w + 4 * m;
+        const bool isq = job >= 10;
+        const int t = isq ? job - 10 : job;
+        const int ti = tile_i(t), tj = tile_j(t);
+        f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const u32x4 a = isq ? *(const u32x4 *)&Qs[16 * ti + lr][ks * 32 + 8 * lg]
+                                : *(const u32x4 *)&Ks[16 * ti + lr][ks * 32 + 8 * lg];
+            const u32x4 bk = *(const u32x4 *)&Ks[16 * tj + lr][ks * 32 + 8 * lg];
+            r = mfma_bf16(a, bk, r);
+        }
+        acc[m] = r;
+        if (isq) {  // P = exp(L_t - L_j) q_t . k_j for j <= t, bf16, block layout
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int tt = 16 * ti + 4 * lg + e, jj = 16 * tj + lr;
+                const float pv = jj <= tt ? expf(Lg[tt] - Lg[jj]) * r[e] : 0.f;
+                Ps[t * kBlk + (4 * lg + e) * 16 + lr] = (bf16_t)f32_to_bf16(pv);
             }
         }
     }
+    lds_barrier();  // K and Q are no longer read: their bytes become A and T
 
-    for (int hh = 0; hh < p.ratio; ++hh) {
-        const int h = g * p.ratio + hh;
-        char *rec = p.records + ((int64_t)c * p.HV + h) * kRecBytes;
-        float *gates = (float *)(rec + kRecGates);
-
-        // Gates and the in-chunk cumulative log decay (wave 0, one lane per token).
-        if (w == 0) {
-            float la = 0.f, bt = 0.f;
-            if (l < len) {
-                const float A_log = p.A_log[h * p.A_log_s];
-                const float dtb = p.dt_bias[h * p.dt_s];
-                const float x = bf16_to_f32(p.a[(int64_t)(tok0 + l) * p.a_st + h * p.a_sh]) + dtb;
-                const float sp = x > 20.f ? x : logf(1.f + expf(x));
-                la = -expf(A_log) * sp;
-                const float bv = bf16_to_f32(p.b[(int64_t)(tok0 + l) * p.b_st + h * p.b_sh]);
-                bt = 1.f / (1.f + expf(-bv));
-            }
-            float L = la;
+    // A[t,j] = beta_t exp(L_t - L_j) k_t . k_j, j < t
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(L, off, 64);
-                if (l >= off)
-                    L += y;
-            }
-            const float Lend = __shfl(L, 63, 64);
-            Lg[l] = L;
-            Bt[l] = bt;
-            gates[l] = bt;
-            gates[64 + l] = expf(L);
-            gates[128 + l] = expf(Lend - L);
-            if (l == 0)
-                gates[192] = expf(Lend);
-        }
-        __syncthreads();
-
-        // A (strictly lower, fp32) -> LDS; P (lower incl., bf16) -> record.
-        bf16_t *Prec = (bf16_t *)(rec + kRecP);
+    for (int m = 0; m < 5; ++m) {
+        const int job = w + 4 * m;
+        if (job < 10) {
+            const int ti = tile_i(job), tj = tile_j(job);
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * w + 4 * lg + i;
-                const int j = 16 * jt + lr;
-                float av = 0.f, pv = 0.f;
-                if (jt <= w && j <= t) {
-                    const float e = expf(Lg[t] - Lg[j]);
-                    pv = e * qk[jt][i];
-                    if (j < t)
-                        av = Bt[t] * e * kk[jt][i];
-                }
-                As[t][j] = av;
-                Prec[t * kC + j] = (bf16_t)f32_to_bf16(pv);
+            for (int e = 0; e < 4; ++e) {
+                const int tt = 16 * ti + 4 * lg + e, jj = 16 * tj + lr;
+                As[tt][jj] = jj < tt ? Bt[tt] * expf(Lg[tt] - Lg[jj]) * acc[m][e] : 0.f;
             }
         }
-        __syncthreads();
+    }
+    for (int q = tid; q < 10 * kBlk / 8; q += 256)
+        *(u32x4 *)(rec + kRecP + q * 16) = *(const u32x4 *)((const char *)Ps + q * 16);
+    lds_barrier();
 
-        // Diagonal 16x16 blocks of T by forward substitution: wave 0, lane =
-        // (block, column).
-        if (w == 0) {
-            const int blk = l >> 4, col = l & 15, o = 16 * blk;
-            float x[16];
+    // Diagonal blocks of T = (I + A)^-1: wave i inverts block i by right-looking
+    // substitution; lane = 4 * column + row group, each lane holding rows g4 + 4m.
+    {
+        const int o = 16 * w, col = l >> 2, g4 = l & 3;
+        float x[4];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float acc = (r == col) ? 1.f : 0.f;
+        for (int m = 0; m < 4; ++m)
+            x[m] = (g4 + 4 * m == col) ? 1.f : 0.f;
 #pragma unroll
-                for (int j = 0; j < r; ++j)
-                    acc = fmaf(-As[o + r][o + j], x[j], acc);
-                x[r] = acc;
-            }
+        for (int r = 0; r < 16; ++r) {
+            const float xr = quad_bcast_sel(x[r >> 2], r & 3);  // final x_r of this column
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                Ts[o + r][o + col] = x[r];
-        } else {
-            // zero the strictly-upper blocks (T is lower triangular)
-            for (int e = tid - 64; e < kC * kC; e += 192) {
-                const int r = e >> 6, cc = e & 63;
-                if ((cc >> 4) > (r >> 4))
-                    Ts[r][cc] = 0.f;
-            }
+            for (int m = 0; m < 4; ++m)  // A is zero on and above the diagonal
+                x[m] = fmaf(-As[o + g4 + 4 * m][o + r], xr, x[m]);
         }
-        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            Ts[o + g4 + 4 * m][o + col] = x[m];
+    }
+    lds_barrier();
 
-        // Off-diagonal blocks, one block diagonal at a time:
-        //   T_ij = -T_ii * sum_{m=j}^{i-1} A_im T_mj      (fp32 MFMA 16x16x4)
-        for (int d = 1; d < 4; ++d) {
-            const int i = w + d, j = w;
-            const bool active = i < 4;
-            if (active) {
-                f32x4 M = {0.f, 0.f, 0.f, 0.f};
-                for (int m = j; m < i; ++m) {
+    // Off-diagonal blocks, one block diagonal at a time (fp32 MFMA 16x16x4):
+    //   T_ij = -T_ii * sum_{m=j}^{i-1} A_im T_mj
+    for (int d = 1; d < 4; ++d) {
+        const int i = w + d, j = w;
+        const bool active = i < 4;
+        if (active) {
+            f32x4 M = {0.f, 0.f, 0.f, 0.f};
+            for (int m = j; m < i; ++m) {
 #pragma unroll
-                    for (int k4 = 0; k4 < 4; ++k4) {
-                        const float av = As[16 * i + lr][16 * m + 4 * k4 + lg];
-                        const float bv = Ts[16 * m + 4 * k4 + lg][16 * j + lr];
-                        M = mfma_f32(av, bv, M);
-                    }
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    Ms[w][4 * lg + e][lr] = M[e];
+                for (int k4 = 0; k4 < 4; ++k4)
+                    M = mfma_f32(As[16 * i + lr][16 * m + 4 * k4 + lg],
+                                 Ts[16 * m + 4 * k4 + lg][16 * j + lr], M);
             }
-            __syncthreads();
-            if (active) {
-                f32x4 R = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int k4 = 0; k4 < 4; ++k4) {
-                    const float av = Ts[16 * i + lr][16 * i + 4 * k4 + lg];
-                    const float bv = Ms[w][4 * k4 + lg][lr];
-                    R = mfma_f32(av, bv, R);
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    Ts[16 * i + 4 * lg + e][16 * j + lr] = -R[e];
-            }
-            __syncthreads();
+            for (int e = 0; e < 4; ++e)
+                Ms[w][4 * lg + e][lr] = M[e];
         }
+        lds_barrier();
+        if (active) {
+            f32x4 R = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k4 = 0; k4 < 4; ++k4)
+                R = mfma_f32(Ts[16 * i + lr][16 * i + 4 * k4 + lg], Ms[w][4 * k4 + lg][lr], R);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                Ts[16 * i + 4 * lg + e][16 * j + lr] = -R[e];
+        }
+        lds_barrier();
+    }
 
-        // T -> record as bf16 hi / lo halves, row-major [64][64].
-        {
-            const int row = tid >> 2, c0 = (tid & 3) * 16;
-            bf16_t *thi = (bf16_t *)(rec + kRecThi) + row * kC + c0;
-            bf16_t *tlo = (bf16_t *)(rec + kRecTlo) + row * kC + c0;
-            uint32_t hw[8], lw[8];
+    // T -> record (bf16 hi / lo, block layout); 16-byte pieces.
+    for (int q = tid; q < 10 * kBlk / 8; q += 256) {
+        const int bidx = q >> 5, row = (q & 31) >> 1, c8 = (q & 1) * 8;
+        const int bi = tile_i(bidx), bj = tile_j(bidx);
+        uint32_t hw[4], lw[4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                uint32_t h0, l0, h1, l1;
-                split_bf16(Ts[row][c0 + 2 * e], h0, l0);
-                split_bf16(Ts[row][c0 + 2 * e + 1], h1, l1);
-                hw[e] = h0 | (h1 << 16);
-                lw[e] = l0 | (l1 << 16);
-            }
-            *(u32x4 *)thi = u32x4{hw[0], hw[1], hw[2], hw[3]};
-            *(u32x4 *)(thi + 8) = u32x4{hw[4], hw[5], hw[6], hw[7]};
-            *(u32x4 *)tlo = u32x4{lw[0], lw[1], lw[2], lw[3]};
-            *(u32x4 *)(tlo + 8) = u32x4{lw[4], lw[5], lw[6], lw[7]};
-        }
-        __syncthreads();
+        for (int e = 0; e < 4; ++e)
+            split_bf16x2(Ts[16 * bi + row][16 * bj + c8 + 2 * e],
+                         Ts[16 * bi + row][16 * bj + c8 + 2 * e + 1], hw[e], lw[e]);
+        *(u32x4 *)(rec + kRecThi + q * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        *(u32x4 *)(rec + kRecTlo + q * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
     }
 }
 
@@ -376,6 +400,16 @@ struct ScanArgs {
     const char *records;
     int HQK, HV, ratio, ngroups;
     float scale;
+};
+
+// One chunk's operands for one lane, loaded a chunk ahead (MFMA A-operand layouts).
+struct ChunkRegs {
+    u32x4 kf[4];         // K rows 16w+lr, columns 32ks + 8lg .. +7
+    u32x4 th[2], tl[2];  // T hi / lo rows 16w+lr, columns 32ks + 8lg .. +7
+    u32x4 pf[2];         // P, same layout as T
+    uint32_t vv[4];      // V[16w + 4lg + i][v0 + lr] (bf16 bits)
+    f32x4 beta, gamma, dec;  // gates of tokens 16w + 4lg + 0..3
+    float gC;
 };
 
 __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
@@ -407,6 +441,53 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
     __shared__ __align__(16) bf16_t WThi[16][kLdT];
     __shared__ __align__(16) bf16_t WTlo[16][kLdT];
 
+    // Per-lane bases, computed once; a chunk advances them by 64 token rows.
+    const int trow = 16 * w + lr;             // token row of this lane's A operands
+    const int tcol = 16 * w + 4 * lg;         // first of this lane's 4 C-layout token rows
+    const bf16_t *kbase = p.k + (int64_t)tok0 * p.k_st + g * p.k_sh + 8 * lg;
+    const bf16_t *qbase = p.q + (int64_t)tok0 * p.q_st + g * p.q_sh + 8 * lg;
+    const bf16_t *vbase = p.v + (int64_t)tok0 * p.v_st + h * p.v_sh + v0 + lr;
+    bf16_t *obase = p.out + (int64_t)tok0 * p.o_st + h * p.o_sh + v0 + (lr & ~1);
+    const char *rbase = p.records + ((int64_t)c0 * p.HV + h) * kRecBytes;
+    const int64_t rstep = (int64_t)p.HV * kRecBytes;
+    // Element offsets of this lane's T / P A-operand pieces; blocks above the diagonal
+    // are not stored and read the record's zero bytes instead.
+    int thoff[2], tloff[2], poff[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int jb = 2 * ks + (lg >> 1);
+        const int o = tri_blk(w, jb) * kBlk + lr * 16 + 8 * (lg & 1);
+        thoff[ks] = jb <= w ? kRecThi / 2 + o : kRecZero / 2;
+        tloff[ks] = jb <= w ? kRecTlo / 2 + o : kRecZero / 2;
+        poff[ks] = jb <= w ? kRecP / 2 + o : kRecZero / 2;
+    }
+
+    // Rows past a chunk's end are clamped to its last token instead of zeroed: they
+    // carry beta = 0 and decay weight 0, so they contribute exactly nothing, and their
+    // outputs are not stored. Every load reads valid memory and stays in flight.
+    auto load_chunk = [&](ChunkRegs &r, int c) {
+        const int lenc = min(kC, len - c * kC);
+        const bf16_t *rec = (const bf16_t *)(rbase + c * rstep);
+        const bf16_t *kp = kbase + (int64_t)(c * kC + min(trow, lenc - 1)) * p.k_st;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            r.kf[ks] = *(const u32x4 *)(kp + ks * 32);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            r.th[ks] = *(const u32x4 *)(rec + thoff[ks]);
+            r.tl[ks] = *(const u32x4 *)(rec + tloff[ks]);
+            r.pf[ks] = *(const u32x4 *)(rec + poff[ks]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            r.vv[i] = vbase[(int64_t)(c * kC + min(tcol + i, lenc - 1)) * p.v_st];
+        const float *gt = (const float *)((const char *)rec + kRecGates);
+        r.beta = *(const f32x4 *)(gt + tcol);
+        r.gamma = *(const f32x4 *)(gt + 64 + tcol);
+        r.dec = *(const f32x4 *)(gt + 128 + tcol);
+        r.gC = gt[192];
+    };
+
     // State tile rows v0..v0+15 in MFMA C layout: Sreg[j][i] = S[v0 + 4 lg + i][16 (2w + j) + lr].
     f32x4 Sreg[2];
 #pragma unroll
@@ -416,154 +497,153 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
             const int vv = v0 + 4 * lg + i, kc = 16 * (2 * w + j) + lr;
             Sreg[j][i] = p.state ? p.state[n * p.st_sn + h * p.st_sh + vv * p.st_sv + kc] : 0.f;
         }
+    // S -> LDS as bf16 hi / lo. Lanes lr and lr^1 hold neighbouring columns: even lanes
+    // store rows 0,1 and odd lanes rows 2,3 of the pair as packed 32-bit words (element
+    // indices stay static: the lane choice only predicates the stores).
+    const bool even = (lr & 1) == 0;
     auto stage_state = [&]() {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
+            const int col = (16 * (2 * w + j) + lr) & ~1;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const float mine = Sreg[j][i];
+                const float oth = dpp_mov<kDppQuadXor1>(mine);
                 uint32_t hi, lo;
-                split_bf16(Sreg[j][i], hi, lo);
-                Shi[4 * lg + i][16 * (2 * w + j) + lr] = (bf16_t)hi;
-                Slo[4 * lg + i][16 * (2 * w + j) + lr] = (bf16_t)lo;
+                split_bf16x2(even ? mine : oth, even ? oth : mine, hi, lo);
+                if (even == (i < 2)) {
+                    *(uint32_t *)&Shi[4 * lg + i][col] = hi;
+                    *(uint32_t *)&Slo[4 * lg + i][col] = lo;
+                }
             }
+        }
     };
     stage_state();
 
-    for (int c = 0; c < nck; ++c) {
-        const int tokc = tok0 + c * kC;
+    auto step = [&](ChunkRegs &cur, ChunkRegs &nxt, int c) {
         const int lenc = min(kC, len - c * kC);
-        const char *rec = p.records + ((int64_t)(c0 + c) * p.HV + h) * kRecBytes;
-        const float *gates = (const float *)(rec + kRecGates);
-
-        // (0) K chunk -> LDS
-        for (int s = tid; s < kC * (kDK / 8); s += 256) {
-            const int row = s >> 4, col = (s & 15) * 8;
-            u32x4 kv = {0u, 0u, 0u, 0u};
-            if (row < lenc)
-                kv = *(const u32x4 *)(p.k + (int64_t)(tokc + row) * p.k_st + g * p.k_sh + col);
-            *(u32x4 *)&Ks[row][col] = kv;
+        if (c + 1 < nck)
+            load_chunk(nxt, c + 1);  // in flight while this chunk computes
+        // Q of this chunk: first needed by the readout (d), after three phases
+        u32x4 qf[4];
+        {
+            const bf16_t *qp = qbase + (int64_t)(c * kC + min(trow, lenc - 1)) * p.q_st;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                qf[ks] = *(const u32x4 *)(qp + ks * 32);
         }
-        __syncthreads();
+
+        // K rows of this wave -> LDS (the state update reads K by columns)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            *(u32x4 *)&Ks[trow][ks * 32 + 8 * lg] = cur.kf[ks];
+        lds_barrier();
 
         // (a) X = K S0^T for tokens 16w..16w+15 (S0 as hi + lo)
         f32x4 X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const u32x4 a = *(const u32x4 *)&Ks[16 * w + lr][ks * 32 + 8 * lg];
             const u32x4 bh = *(const u32x4 *)&Shi[lr][ks * 32 + 8 * lg];
             const u32x4 bl = *(const u32x4 *)&Slo[lr][ks * 32 + 8 * lg];
-            X = mfma_bf16(a, bh, X);
-            X = mfma_bf16(a, bl, X);
+            X = mfma_bf16(cur.kf[ks], bh, X);
+            X = mfma_bf16(cur.kf[ks], bl, X);
         }
-        // (b) R = beta (V - gamma X)  -> LDS as R^T (hi, lo)
-        float gam[4];
+        // (b) R = beta (V - gamma X) -> LDS as R^T (hi, lo)
         {
-            uint32_t rh[4], rl[4];
+            float r[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * w + 4 * lg + i;
-                const float vv = t < lenc
-                    ? bf16_to_f32(p.v[(int64_t)(tokc + t) * p.v_st + h * p.v_sh + v0 + lr])
-                    : 0.f;
-                gam[i] = gates[64 + t];
-                const float r = gates[t] * (vv - gam[i] * X[i]);
-                split_bf16(r, rh[i], rl[i]);
-            }
-            *(u32x2 *)&RThi[lr][16 * w + 4 * lg] = u32x2{rh[0] | (rh[1] << 16), rh[2] | (rh[3] << 16)};
-            *(u32x2 *)&RTlo[lr][16 * w + 4 * lg] = u32x2{rl[0] | (rl[1] << 16), rl[2] | (rl[3] << 16)};
+            for (int i = 0; i < 4; ++i)
+                r[i] = cur.beta[i] * (bf16_to_f32(cur.vv[i]) - cur.gamma[i] * X[i]);
+            uint32_t h01, l01, h23, l23;
+            split_bf16x2(r[0], r[1], h01, l01);
+            split_bf16x2(r[2], r[3], h23, l23);
+            *(u32x2 *)&RThi[lr][tcol] = u32x2{h01, h23};
+            *(u32x2 *)&RTlo[lr][tcol] = u32x2{l01, l23};
         }
-        __syncthreads();
+        lds_barrier();
 
-        // (c) U = T R  (T, R as hi + lo; three products)
+        // (c) U = T R  (T, R as hi + lo; three products). Rows < 32 of T have no
+        // entries in columns >= 32.
         f32x4 U = {0.f, 0.f, 0.f, 0.f};
-        {
-            const bf16_t *thi = (const bf16_t *)(rec + kRecThi);
-            const bf16_t *tlo = (const bf16_t *)(rec + kRecTlo);
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                if (ks == 1 && w < 2)
-                    continue;  // T rows < 32 have no entries in columns >= 32
-                const u32x4 ah = *(const u32x4 *)(thi + (16 * w + lr) * kC + ks * 32 + 8 * lg);
-                const u32x4 al = *(const u32x4 *)(tlo + (16 * w + lr) * kC + ks * 32 + 8 * lg);
-                const u32x4 bh = *(const u32x4 *)&RThi[lr][ks * 32 + 8 * lg];
-                const u32x4 bl = *(const u32x4 *)&RTlo[lr][ks * 32 + 8 * lg];
-                U = mfma_bf16(ah, bh, U);
-                U = mfma_bf16(ah, bl, U);
-                U = mfma_bf16(al, bh, U);
-            }
-            uint32_t uh[4], wh[4], wl[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * w + 4 * lg + i;
-                uh[i] = f32_to_bf16(U[i]);
-                split_bf16(gates[128 + t] * U[i], wh[i], wl[i]);
-            }
-            *(u32x2 *)&UThi[lr][16 * w + 4 * lg] = u32x2{uh[0] | (uh[1] << 16), uh[2] | (uh[3] << 16)};
-            *(u32x2 *)&WThi[lr][16 * w + 4 * lg] = u32x2{wh[0] | (wh[1] << 16), wh[2] | (wh[3] << 16)};
-            *(u32x2 *)&WTlo[lr][16 * w + 4 * lg] = u32x2{wl[0] | (wl[1] << 16), wl[2] | (wl[3] << 16)};
+        for (int ks = 0; ks < 2; ++ks) {
+            if (ks == 1 && w < 2)
+                continue;
+            const u32x4 bh = *(const u32x4 *)&RThi[lr][ks * 32 + 8 * lg];
+            const u32x4 bl = *(const u32x4 *)&RTlo[lr][ks * 32 + 8 * lg];
+            U = mfma_bf16(cur.th[ks], bh, U);
+            U = mfma_bf16(cur.th[ks], bl, U);
+            U = mfma_bf16(cur.tl[ks], bh, U);
         }
-        __syncthreads();
+        {
+            uint32_t wh01, wl01, wh23, wl23;
+            split_bf16x2(cur.dec[0] * U[0], cur.dec[1] * U[1], wh01, wl01);
+            split_bf16x2(cur.dec[2] * U[2], cur.dec[3] * U[3], wh23, wl23);
+            *(u32x2 *)&UThi[lr][tcol] = u32x2{pack_bf16x2(U[0], U[1]), pack_bf16x2(U[2], U[3])};
+            *(u32x2 *)&WThi[lr][tcol] = u32x2{wh01, wh23};
+            *(u32x2 *)&WTlo[lr][tcol] = u32x2{wl01, wl23};
+        }
+        lds_barrier();
 
         // (d) O = scale (gamma Q S0^T + P U) for tokens 16w..16w+15
         {
             f32x4 Oi = {0.f, 0.f, 0.f, 0.f}, Oa = {0.f, 0.f, 0.f, 0.f};
-            const int trow = 16 * w + lr;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                u32x4 aq = {0u, 0u, 0u, 0u};
-                if (trow < lenc)
-                    aq = *(const u32x4 *)(p.q + (int64_t)(tokc + trow) * p.q_st + g * p.q_sh +
-                                          ks * 32 + 8 * lg);
-                const u32x4 bh = *(const u32x4 *)&Shi[lr][ks * 32 + 8 * lg];
-                Oi = mfma_bf16(aq, bh, Oi);
-            }
-            const bf16_t *prec = (const bf16_t *)(rec + kRecP);
+            for (int ks = 0; ks < 4; ++ks)
+                Oi = mfma_bf16(qf[ks], *(const u32x4 *)&Shi[lr][ks * 32 + 8 * lg], Oi);
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 if (ks == 1 && w < 2)
                     continue;
-                const u32x4 ap = *(const u32x4 *)(prec + trow * kC + ks * 32 + 8 * lg);
-                const u32x4 bu = *(const u32x4 *)&UThi[lr][ks * 32 + 8 * lg];
-                Oa = mfma_bf16(ap, bu, Oa);
+                Oa = mfma_bf16(cur.pf[ks], *(const u32x4 *)&UThi[lr][ks * 32 + 8 * lg], Oa);
             }
+            // lanes lr, lr^1 pack neighbouring columns: even lanes store rows 0,1, odd 2,3
+            bf16_t *op = obase + c * (int64_t)kC * p.o_st;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int t = 16 * w + 4 * lg + i;
-                if (t < lenc)
-                    p.out[(int64_t)(tokc + t) * p.o_st + h * p.o_sh + v0 + lr] =
-                        (bf16_t)f32_to_bf16(p.scale * fmaf(gam[i], Oi[i], Oa[i]));
+                const float mine = p.scale * fmaf(cur.gamma[i], Oi[i], Oa[i]);
+                const float oth = dpp_mov<kDppQuadXor1>(mine);
+                const uint32_t packed = pack_bf16x2(even ? mine : oth, even ? oth : mine);
+                if (even == (i < 2) && tcol + i < lenc)
+                    *(uint32_t *)(op + (int64_t)(tcol + i) * p.o_st) = packed;
             }
         }
 
         // (e) S = gammaC S + W^T K over this wave's 32 state columns
-        {
-            const float gC = gates[192];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int kc = 16 * (2 * w + j) + lr;
-                f32x4 dS = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 2; ++j) {
+            const int kc = 16 * (2 * w + j) + lr;
+            f32x4 dS = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const u32x4 awh = *(const u32x4 *)&WThi[lr][ks * 32 + 8 * lg];
-                    const u32x4 awl = *(const u32x4 *)&WTlo[lr][ks * 32 + 8 * lg];
-                    uint32_t kw[4];
+            for (int ks = 0; ks < 2; ++ks) {
+                const u32x4 awh = *(const u32x4 *)&WThi[lr][ks * 32 + 8 * lg];
+                const u32x4 awl = *(const u32x4 *)&WTlo[lr][ks * 32 + 8 * lg];
+                uint32_t kw[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t k0 = Ks[ks * 32 + 8 * lg + 2 * e][kc];
-                        const uint32_t k1 = Ks[ks * 32 + 8 * lg + 2 * e + 1][kc];
-                        kw[e] = k0 | (k1 << 16);
-                    }
-                    const u32x4 bk = {kw[0], kw[1], kw[2], kw[3]};
-                    dS = mfma_bf16(awh, bk, dS);
-                    dS = mfma_bf16(awl, bk, dS);
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t k0 = Ks[ks * 32 + 8 * lg + 2 * e][kc];
+                    const uint32_t k1 = Ks[ks * 32 + 8 * lg + 2 * e + 1][kc];
+                    kw[e] = k0 | (k1 << 16);
                 }
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    Sreg[j][i] = fmaf(gC, Sreg[j][i], dS[i]);
+                const u32x4 bk = {kw[0], kw[1], kw[2], kw[3]};
+                dS = mfma_bf16(awh, bk, dS);
+                dS = mfma_bf16(awl, bk, dS);
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                Sreg[j][i] = fmaf(cur.gC, Sreg[j][i], dS[i]);
         }
-        __syncthreads();
+        lds_barrier();
         stage_state();
+    };
+
+    ChunkRegs ra, rb;
+    if (nck > 0)
+        load_chunk(ra, 0);
+    for (int c = 0; c < nck; c += 2) {
+        step(ra, rb, c);
+        if (c + 1 < nck)
+            step(rb, ra, c + 1);
     }
 
 #pragma unroll
@@ -721,11 +801,14 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         qa.chunk_tok0 = pa.chunk_tok0;
         qa.chunk_len = pa.chunk_len;
         qa.records = ws + L.records;
+        qa.HQK = HQK;
         qa.HV = HV;
         qa.ratio = ratio;
-        if (L.nc > 0x7fffffff || HQK > 65535)
+        const int64_t units = L.nc * HQK;  // (chunk, q/k head) groups
+        const int64_t blocks = 8 * (int64_t)ratio * ((units + 7) / 8);
+        if (blocks > 0x7fffffff)
             return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
-        hipLaunchKernelGGL(gdn::gdn_prefill_prep_kernel, dim3((unsigned)L.nc, HQK), dim3(256), 0,
+        hipLaunchKernelGGL(gdn::gdn_prefill_prep_kernel, dim3((unsigned)blocks), dim3(256), 0,
                            st, qa);
         rc = gdn_check_launch("gdn_prefill_prep_kernel");
         if (rc)
