@@ -412,7 +412,8 @@ struct ChunkRegs {
     float gC;
 };
 
-__global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gdn_prefill_scan_kernel(ScanArgs p)
 {
     // Workgroups of one (sequence, q/k head) group share K, Q, T and P through L2:
     // place them on one XCD (workgroup ids are dealt to the 8 XCDs round-robin).
@@ -539,15 +540,17 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
             *(u32x4 *)&Ks[trow][ks * 32 + 8 * lg] = cur.kf[ks];
         lds_barrier();
 
-        // (a) X = K S0^T for tokens 16w..16w+15 (S0 as hi + lo)
-        f32x4 X = {0.f, 0.f, 0.f, 0.f};
+        // (a) X = K S0^T for tokens 16w..16w+15 (S0 as hi + lo; two accumulators keep
+        // the dependent MFMA chains short)
+        f32x4 X = {0.f, 0.f, 0.f, 0.f}, Xl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const u32x4 bh = *(const u32x4 *)&Shi[lr][ks * 32 + 8 * lg];
             const u32x4 bl = *(const u32x4 *)&Slo[lr][ks * 32 + 8 * lg];
             X = mfma_bf16(cur.kf[ks], bh, X);
-            X = mfma_bf16(cur.kf[ks], bl, X);
+            Xl = mfma_bf16(cur.kf[ks], bl, Xl);
         }
+        X += Xl;
         // (b) R = beta (V - gamma X) -> LDS as R^T (hi, lo)
         {
             float r[4];
@@ -564,7 +567,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
 
         // (c) U = T R  (T, R as hi + lo; three products). Rows < 32 of T have no
         // entries in columns >= 32.
-        f32x4 U = {0.f, 0.f, 0.f, 0.f};
+        f32x4 U = {0.f, 0.f, 0.f, 0.f}, Ul = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             if (ks == 1 && w < 2)
@@ -572,9 +575,10 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
             const u32x4 bh = *(const u32x4 *)&RThi[lr][ks * 32 + 8 * lg];
             const u32x4 bl = *(const u32x4 *)&RTlo[lr][ks * 32 + 8 * lg];
             U = mfma_bf16(cur.th[ks], bh, U);
-            U = mfma_bf16(cur.th[ks], bl, U);
-            U = mfma_bf16(cur.tl[ks], bh, U);
+            Ul = mfma_bf16(cur.th[ks], bl, Ul);
+            Ul = mfma_bf16(cur.tl[ks], bh, Ul);
         }
+        U += Ul;
         {
             uint32_t wh01, wl01, wh23, wl23;
             split_bf16x2(cur.dec[0] * U[0], cur.dec[1] * U[1], wh01, wl01);
@@ -613,7 +617,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int kc = 16 * (2 * w + j) + lr;
-            f32x4 dS = {0.f, 0.f, 0.f, 0.f};
+            f32x4 dS = {0.f, 0.f, 0.f, 0.f}, dSl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const u32x4 awh = *(const u32x4 *)&WThi[lr][ks * 32 + 8 * lg];
@@ -627,8 +631,9 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan_kernel(ScanArgs p)
                 }
                 const u32x4 bk = {kw[0], kw[1], kw[2], kw[3]};
                 dS = mfma_bf16(awh, bk, dS);
-                dS = mfma_bf16(awl, bk, dS);
+                dSl = mfma_bf16(awl, bk, dSl);
             }
+            dS += dSl;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 Sreg[j][i] = fmaf(cur.gC, Sreg[j][i], dS[i]);
