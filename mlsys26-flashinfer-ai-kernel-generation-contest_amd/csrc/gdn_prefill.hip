@@ -233,15 +233,30 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
 
     char *rec = p.records + ((int64_t)c * p.HV + h) * kRecBytes;
 
-    for (int s = tid; s < kC * (kDK / 8); s += 256) {
-        const int row = s >> 4, col = (s & 15) * 8;
-        u32x4 kv = {0u, 0u, 0u, 0u}, qv = {0u, 0u, 0u, 0u};
-        if (row < len) {
-            kv = *(const u32x4 *)(p.k + (int64_t)(tok0 + row) * p.k_st + g * p.k_sh + col);
-            qv = *(const u32x4 *)(p.q + (int64_t)(tok0 + row) * p.q_st + g * p.q_sh + col);
+    // Wave 0's gate inputs (one token per lane) are requested first, then K and Q.
+    uint32_t a_raw = 0u, b_raw = 0u;
+    if (w == 0) {
+        const int t = tok0 + min(l, len - 1);
+        a_raw = p.a[(int64_t)t * p.a_st + h * p.a_sh];
+        b_raw = p.b[(int64_t)t * p.b_st + h * p.b_sh];
+    }
+    // K, Q chunk rows -> LDS. All eight 16-byte loads per lane are issued before the
+    // first store. Rows past the chunk's end repeat its last token: they only meet
+    // beta = 0 (in A) or the causal mask (in P), so they contribute nothing.
+    {
+        u32x4 kv[4], qv[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int s = tid + 256 * m, row = min(s >> 4, len - 1), col = (s & 15) * 8;
+            kv[m] = *(const u32x4 *)(p.k + (int64_t)(tok0 + row) * p.k_st + g * p.k_sh + col);
+            qv[m] = *(const u32x4 *)(p.q + (int64_t)(tok0 + row) * p.q_st + g * p.q_sh + col);
         }
-        *(u32x4 *)&Ks[row][col] = kv;
-        *(u32x4 *)&Qs[row][col] = qv;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int s = tid + 256 * m, row = s >> 4, col = (s & 15) * 8;
+            *(u32x4 *)&Ks[row][col] = kv[m];
+            *(u32x4 *)&Qs[row][col] = qv[m];
+        }
     }
 
     // Gates and in-chunk cumulative log decay: wave 0, one lane per token
@@ -249,15 +264,14 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
     if (w == 0) {
         float la = 0.f, bt = 0.f;
         if (l < len) {
-            const float A_log = p.A_log[h * p.A_log_s];
-            const float dtb = p.dt_bias[h * p.dt_s];
-            const float x = bf16_to_f32(p.a[(int64_t)(tok0 + l) * p.a_st + h * p.a_sh]) + dtb;
+            const float x = bf16_to_f32(a_raw) + p.dt_bias[h * p.dt_s];
             const float sp = x > 20.f ? x : logf(1.f + expf(x));
-            la = -expf(A_log) * sp;
-            const float bv = bf16_to_f32(p.b[(int64_t)(tok0 + l) * p.b_st + h * p.b_sh]);
-            bt = 1.f / (1.f + expf(-bv));
+            la = -expf(p.A_log[h * p.A_log_s]) * sp;
+            bt = 1.f / (1.f + expf(-bf16_to_f32(b_raw)));
         }
-        float L = la;
+        // cumulative decay in log2 units: every decay factor below is 2^(non-positive
+        // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow)
+        float L = la * 1.44269504088896340736f;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const float y = __shfl_up(L, off, 64);
@@ -269,10 +283,10 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
         Bt[l] = bt;
         float *gates = (float *)(rec + kRecGates);
         gates[l] = bt;
-        gates[64 + l] = expf(L);
-        gates[128 + l] = expf(Lend - L);
+        gates[64 + l] = __builtin_amdgcn_exp2f(L);
+        gates[128 + l] = __builtin_amdgcn_exp2f(Lend - L);
         if (l == 0)
-            gates[192] = expf(Lend);
+            gates[192] = __builtin_amdgcn_exp2f(Lend);
         if (l < 4)
             ((float *)(rec + kRecZero))[l] = 0.f;
     }
@@ -299,7 +313,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tt = 16 * ti + 4 * lg + e, jj = 16 * tj + lr;
-                const float pv = jj <= tt ? expf(Lg[tt] - Lg[jj]) * r[e] : 0.f;
+                const float pv = jj <= tt ? __builtin_amdgcn_exp2f(Lg[tt] - Lg[jj]) * r[e] : 0.f;
                 Ps[t * kBlk + (4 * lg + e) * 16 + lr] = (bf16_t)f32_to_bf16(pv);
             }
         }
@@ -315,7 +329,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tt = 16 * ti + 4 * lg + e, jj = 16 * tj + lr;
-                As[tt][jj] = jj < tt ? Bt[tt] * expf(Lg[tt] - Lg[jj]) * acc[m][e] : 0.f;
+                As[tt][jj] = jj < tt ? Bt[tt] * __builtin_amdgcn_exp2f(Lg[tt] - Lg[jj]) * acc[m][e] : 0.f;
             }
         }
     }
@@ -442,51 +456,63 @@ gdn_prefill_scan_kernel(ScanArgs p)
     __shared__ __align__(16) bf16_t WThi[16][kLdT];
     __shared__ __align__(16) bf16_t WTlo[16][kLdT];
 
-    // Per-lane bases, computed once; a chunk advances them by 64 token rows.
+    // Addressing: per chunk a wave-uniform 64-bit base (scalar registers) plus a 32-bit
+    // per-lane byte offset (the host keeps token / head strides below 2^24 elements),
+    // so loads and stores use the scalar-base + vector-offset form.
     const int trow = 16 * w + lr;             // token row of this lane's A operands
     const int tcol = 16 * w + 4 * lg;         // first of this lane's 4 C-layout token rows
-    const bf16_t *kbase = p.k + (int64_t)tok0 * p.k_st + g * p.k_sh + 8 * lg;
-    const bf16_t *qbase = p.q + (int64_t)tok0 * p.q_st + g * p.q_sh + 8 * lg;
-    const bf16_t *vbase = p.v + (int64_t)tok0 * p.v_st + h * p.v_sh + v0 + lr;
-    bf16_t *obase = p.out + (int64_t)tok0 * p.o_st + h * p.o_sh + v0 + (lr & ~1);
+    const uint32_t kst2 = (uint32_t)p.k_st * 2, qst2 = (uint32_t)p.q_st * 2;
+    const uint32_t vst2 = (uint32_t)p.v_st * 2, ost2 = (uint32_t)p.o_st * 2;
+    const char *kbase = (const char *)(p.k + (int64_t)tok0 * p.k_st + g * p.k_sh);
+    const char *qbase = (const char *)(p.q + (int64_t)tok0 * p.q_st + g * p.q_sh);
+    const char *vbase = (const char *)(p.v + (int64_t)tok0 * p.v_st + h * p.v_sh);
+    char *obase = (char *)(p.out + (int64_t)tok0 * p.o_st + h * p.o_sh);
+    const int64_t kstep = (int64_t)kC * p.k_st * 2, qstep = (int64_t)kC * p.q_st * 2;
+    const int64_t vstep = (int64_t)kC * p.v_st * 2, ostep = (int64_t)kC * p.o_st * 2;
     const char *rbase = p.records + ((int64_t)c0 * p.HV + h) * kRecBytes;
     const int64_t rstep = (int64_t)p.HV * kRecBytes;
-    // Element offsets of this lane's T / P A-operand pieces; blocks above the diagonal
-    // are not stored and read the record's zero bytes instead.
-    int thoff[2], tloff[2], poff[2];
+    // Byte offsets of this lane's T / P A-operand pieces inside a record; blocks above
+    // the diagonal are not stored and read the record's zero bytes instead.
+    uint32_t thoff[2], tloff[2], poff[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
         const int jb = 2 * ks + (lg >> 1);
-        const int o = tri_blk(w, jb) * kBlk + lr * 16 + 8 * (lg & 1);
-        thoff[ks] = jb <= w ? kRecThi / 2 + o : kRecZero / 2;
-        tloff[ks] = jb <= w ? kRecTlo / 2 + o : kRecZero / 2;
-        poff[ks] = jb <= w ? kRecP / 2 + o : kRecZero / 2;
+        const uint32_t o = 2u * (tri_blk(w, jb) * kBlk + lr * 16 + 8 * (lg & 1));
+        thoff[ks] = jb <= w ? kRecThi + o : kRecZero;
+        tloff[ks] = jb <= w ? kRecTlo + o : kRecZero;
+        poff[ks] = jb <= w ? kRecP + o : kRecZero;
     }
+    const uint32_t lane_col = 16u * lg;                 // 8 bf16 per lane group
+    const uint32_t v_col = 2u * (v0 + lr);
+    const uint32_t o_col = 2u * (v0 + (lr & ~1));
+    const uint32_t g_off = 4u * tcol;
 
     // Rows past a chunk's end are clamped to its last token instead of zeroed: they
     // carry beta = 0 and decay weight 0, so they contribute exactly nothing, and their
     // outputs are not stored. Every load reads valid memory and stays in flight.
     auto load_chunk = [&](ChunkRegs &r, int c) {
         const int lenc = min(kC, len - c * kC);
-        const bf16_t *rec = (const bf16_t *)(rbase + c * rstep);
-        const bf16_t *kp = kbase + (int64_t)(c * kC + min(trow, lenc - 1)) * p.k_st;
+        const char *rec = rbase + c * rstep;
+        const char *kc_ = kbase + c * kstep;
+        const uint32_t ko = (uint32_t)min(trow, lenc - 1) * kst2 + lane_col;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-            r.kf[ks] = *(const u32x4 *)(kp + ks * 32);
+            r.kf[ks] = *(const u32x4 *)(kc_ + ko + 64 * ks);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             r.th[ks] = *(const u32x4 *)(rec + thoff[ks]);
             r.tl[ks] = *(const u32x4 *)(rec + tloff[ks]);
             r.pf[ks] = *(const u32x4 *)(rec + poff[ks]);
         }
+        const char *vc_ = vbase + c * vstep;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            r.vv[i] = vbase[(int64_t)(c * kC + min(tcol + i, lenc - 1)) * p.v_st];
-        const float *gt = (const float *)((const char *)rec + kRecGates);
-        r.beta = *(const f32x4 *)(gt + tcol);
-        r.gamma = *(const f32x4 *)(gt + 64 + tcol);
-        r.dec = *(const f32x4 *)(gt + 128 + tcol);
-        r.gC = gt[192];
+            r.vv[i] = *(const bf16_t *)(vc_ + (uint32_t)min(tcol + i, lenc - 1) * vst2 + v_col);
+        const char *gt = rec + kRecGates;
+        r.beta = *(const f32x4 *)(gt + g_off);
+        r.gamma = *(const f32x4 *)(gt + 256 + g_off);
+        r.dec = *(const f32x4 *)(gt + 512 + g_off);
+        r.gC = *(const float *)(gt + 768);
     };
 
     // State tile rows v0..v0+15 in MFMA C layout: Sreg[j][i] = S[v0 + 4 lg + i][16 (2w + j) + lr].
@@ -528,10 +554,11 @@ gdn_prefill_scan_kernel(ScanArgs p)
         // Q of this chunk: first needed by the readout (d), after three phases
         u32x4 qf[4];
         {
-            const bf16_t *qp = qbase + (int64_t)(c * kC + min(trow, lenc - 1)) * p.q_st;
+            const char *qc_ = qbase + c * qstep;
+            const uint32_t qo = (uint32_t)min(trow, lenc - 1) * qst2 + lane_col;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
-                qf[ks] = *(const u32x4 *)(qp + ks * 32);
+                qf[ks] = *(const u32x4 *)(qc_ + qo + 64 * ks);
         }
 
         // K rows of this wave -> LDS (the state update reads K by columns)
@@ -602,14 +629,14 @@ gdn_prefill_scan_kernel(ScanArgs p)
                 Oa = mfma_bf16(cur.pf[ks], *(const u32x4 *)&UThi[lr][ks * 32 + 8 * lg], Oa);
             }
             // lanes lr, lr^1 pack neighbouring columns: even lanes store rows 0,1, odd 2,3
-            bf16_t *op = obase + c * (int64_t)kC * p.o_st;
+            char *oc_ = obase + c * ostep;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float mine = p.scale * fmaf(cur.gamma[i], Oi[i], Oa[i]);
                 const float oth = dpp_mov<kDppQuadXor1>(mine);
                 const uint32_t packed = pack_bf16x2(even ? mine : oth, even ? oth : mine);
                 if (even == (i < 2) && tcol + i < lenc)
-                    *(uint32_t *)(op + (int64_t)(tcol + i) * p.o_st) = packed;
+                    *(uint32_t *)(oc_ + (uint32_t)(tcol + i) * ost2 + o_col) = packed;
             }
         }
 
@@ -742,6 +769,15 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
                                  "gdn_prefill: q/k/output strides must be multiples of 8");
     if (!aligned(p->q, 16) || !aligned(p->k, 16) || !aligned(p->output, 16))
         return gdn_set_error(GDN_ELAYOUT, "gdn_prefill: q/k/output must be 16-byte aligned");
+    // the kernels address a 64-token chunk with 32-bit byte offsets
+    const int64_t kMaxStride = int64_t(1) << 24;
+    for (int i = 0; i < 2; ++i)
+        if (p->q_stride[i] >= kMaxStride || p->k_stride[i] >= kMaxStride ||
+            p->v_stride[i] >= kMaxStride || p->output_stride[i] >= kMaxStride ||
+            p->q_stride[i] < 0 || p->k_stride[i] < 0 || p->v_stride[i] < 0 ||
+            p->output_stride[i] < 0)
+            return gdn_set_error(GDN_ELAYOUT,
+                                 "gdn_prefill: token / head strides must be in [0, 2^24)");
     const Layout L = layout(T, N, HV);
     if (L.nc > 0x7fffffff)
         return gdn_set_error(GDN_EINVAL, "gdn_prefill: too many chunks");
