@@ -86,18 +86,19 @@ def bench_decode(steps, warmup, batch=64, nsets=4):
     return dict(ms=ms, gbs=gbs, bytes=nbytes, trials=trials)
 
 
-def bench_prefill(steps, warmup):
+def bench_prefill(steps, warmup, lens=None, with_state=True):
+    """Prefill over `lens` (default: 16 sequences, lengths ~U[64,1024] from seed 0)."""
     import torch
 
     from gdn_hip import gdn_prefill
     from gdn_hip.inputs import prefill_flops, prefill_inputs, varlen_lengths
 
     dev = torch.device("cuda", 0)
-    lens = varlen_lengths(16, seed=0)
-    inp = prefill_inputs(lens, seed=0, with_state=True).to(dev)
+    lens = lens or varlen_lengths(16, seed=0)
+    inp = prefill_inputs(lens, seed=0, with_state=with_state).to(dev)
     T = sum(lens)
     out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=dev)
-    ns = torch.empty_like(inp.state)
+    ns = torch.empty((len(lens), 32, 128, 128), dtype=torch.float32, device=dev)
     for _ in range(warmup):
         gdn_prefill(*inp.args(), output=out, new_state=ns)
     torch.cuda.synchronize()
@@ -198,6 +199,8 @@ def main():
         pre = bench_prefill(psteps, 2)
         log(f"prefill: T={pre['tokens']} {pre['ms'] * 1e3:.1f} us/step "
             f"{pre['mtok_s']:.1f} Mtok/s {pre['tflops']:.1f} TFLOP/s")
+        pre4k = bench_prefill(psteps, 2, lens=[4096], with_state=False)
+        log(f"prefill 1x4096: {pre4k['ms'] * 1e3:.1f} us/step {pre4k['tflops']:.1f} TFLOP/s")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (decode B=64, fp32 C oracle)")
@@ -235,6 +238,13 @@ def main():
         "cpu_baseline": cpu,
     }
     if pre is not None:
+        rec["prefill_single_4k"] = {
+            "workload": "GDN prefill, 1 sequence x 4096 tokens, zero initial state",
+            "us_per_step": round(pre4k["ms"] * 1e3, 2),
+            "mtok_per_s": round(pre4k["mtok_s"], 2),
+            "tflops": round(pre4k["tflops"], 2),
+            "mfma_frac": round(pre4k["mfma_frac"], 4),
+        }
         rec["prefill"] = {
             "workload": f"GDN prefill, {pre['nseqs']} sequences, lengths ~U[64,1024] (seed 0), "
                         f"T={pre['tokens']} tokens, non-zero fp32 initial state",

@@ -10,11 +10,12 @@
 // (gdn_decode/solution/triton/kernel.py:120-131,165-170,216-218) with the readout
 // S' q expanded so that it needs no second sweep over S'.
 //
-// Thread mapping: a workgroup of 256 lanes covers 32 state rows per pass; each
+// Thread mapping (default): a workgroup of 256 lanes covers 32 state rows; each
 // row is spread over 8 consecutive lanes and each lane owns 16 columns as four
 // float4 at columns 4s + 32j (s = lane % 8, j = 0..3), so one load instruction
 // of a wavefront covers eight full 128-byte row segments. Row sums are 8-lane
-// DPP reductions. RPT passes per workgroup -> 32*RPT rows per workgroup.
+// DPP reductions. Tuning variants change the workgroup size, lanes per row
+// (8 or 16) and rows per lane.
 #include "gdn_common.h"
 
 namespace gdn {
@@ -38,8 +39,6 @@ struct DecodeArgs {
     float scale;
 };
 
-constexpr int kDecThreads = 256;
-constexpr int kDecRowsPerPass = kDecThreads / 8;
 constexpr int kD = 128;
 
 template <bool NT>
@@ -60,20 +59,24 @@ __device__ __forceinline__ void st4(float *p, f32x4 x)
         *reinterpret_cast<f32x4 *>(p) = x;
 }
 
-// Loads 4 consecutive bf16 (8 bytes) and widens them.
-__device__ __forceinline__ void ld_bf16x4(const bf16_t *p, float *dst)
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x)
 {
-    u32x2 w = *reinterpret_cast<const u32x2 *>(p);
-    dst[0] = bf16lo(w.x);
-    dst[1] = bf16hi(w.x);
-    dst[2] = bf16lo(w.y);
-    dst[3] = bf16hi(w.y);
+    if constexpr (LPR == 8)
+        return group8_sum(x);
+    else
+        return group16_sum(x);
 }
 
-template <int RPT, bool NT, bool HAS_STATE>
-__global__ __launch_bounds__(kDecThreads) void gdn_decode_kernel(DecodeArgs p)
+// THREADS lanes per workgroup, LPR lanes per state row (8 or 16), RPT rows per lane.
+// Lane s of a row owns the float4 column groups 4s + 4*LPR*j, j < NV4.
+template <int THREADS, int LPR, int RPT, bool NT, bool HAS_STATE>
+__global__ __launch_bounds__(THREADS) void gdn_decode_kernel(DecodeArgs p)
 {
-    constexpr int kNVT = kD / (kDecRowsPerPass * RPT);  // workgroups per state
+    constexpr int kRowsPerPass = THREADS / LPR;
+    constexpr int kNV4 = kD / (4 * LPR);             // float4 per lane per row
+    constexpr int kNVT = kD / (kRowsPerPass * RPT);  // workgroups per state
+    constexpr int kCols = 4 * kNV4;                  // columns per lane
     const int bid = blockIdx.x;
     const int vt = bid % kNVT;
     const int bh = bid / kNVT;
@@ -81,73 +84,96 @@ __global__ __launch_bounds__(kDecThreads) void gdn_decode_kernel(DecodeArgs p)
     const int bi = bh / p.HV;
     const int g = h / p.ratio;  // GVA: q/k head of this v-head (kernel.py:120)
     const int tid = threadIdx.x;
-    const int s = tid & 7;
-    const int rg = tid >> 3;
+    const int s = tid % LPR;
+    const int rg = tid / LPR;
 
-    // Gates (gdn_decode/solution/triton/kernel.py:123-131).
-    const float A_log = p.A_log[h * p.A_log_s];
-    const float dtb = p.dt_bias[h * p.dt_s];
-    const float av = bf16_to_f32(p.a[bi * p.a_sb + h * p.a_sh]);
-    const float bv = bf16_to_f32(p.b[bi * p.b_sb + h * p.b_sh]);
-    const float x = av + dtb;
-    const float sp = x > 20.f ? x : logf(1.f + expf(x));
-    const float alpha = expf(-expf(A_log) * sp);
-    const float beta = 1.f / (1.f + expf(-bv));
+    const int v0 = vt * kRowsPerPass * RPT;
 
-    const int v0 = vt * kDecRowsPerPass * RPT;
-
-    // Issue the state loads first: they are the bytes that matter.
-    f32x4 S[RPT][4];
-    if constexpr (HAS_STATE) {
-        const float *sbase = p.state + bi * p.st_sb + h * p.st_sh;
-#pragma unroll
-        for (int r = 0; r < RPT; ++r) {
-            const float *row = sbase + (int64_t)(v0 + rg + kDecRowsPerPass * r) * p.st_sv + 4 * s;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                S[r][j] = ld4<NT>(row + 32 * j);
-        }
-    }
-
-    float kk[16], qq[16];
+    // Load order matters: vector loads return in issue order, so the few small loads
+    // (gates, k, q, v) go first and the state stream right after; the gate math then
+    // waits only for the small ones while the state is still in flight.
+    const uint32_t a_raw = p.a[bi * p.a_sb + h * p.a_sh];
+    const uint32_t b_raw = p.b[bi * p.b_sb + h * p.b_sh];
+    u32x2 kraw[kNV4], qraw[kNV4];
     {
         const bf16_t *kp = p.k + bi * p.k_sb + g * p.k_sh + 4 * s;
         const bf16_t *qp = p.q + bi * p.q_sb + g * p.q_sh + 4 * s;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            ld_bf16x4(kp + 32 * j, kk + 4 * j);
-            ld_bf16x4(qp + 32 * j, qq + 4 * j);
+        for (int j = 0; j < kNV4; ++j) {
+            kraw[j] = *reinterpret_cast<const u32x2 *>(kp + 4 * LPR * j);
+            qraw[j] = *reinterpret_cast<const u32x2 *>(qp + 4 * LPR * j);
         }
+    }
+    uint32_t vraw[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r)
+        vraw[r] = p.v[bi * p.v_sb + h * p.v_sh + v0 + rg + kRowsPerPass * r];
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 S[RPT][kNV4];
+    if constexpr (HAS_STATE) {
+        const float *sbase = p.state + bi * p.st_sb + h * p.st_sh;
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const float *row = sbase + (int64_t)(v0 + rg + kRowsPerPass * r) * p.st_sv + 4 * s;
+#pragma unroll
+            for (int j = 0; j < kNV4; ++j)
+                S[r][j] = ld4<NT>(row + 4 * LPR * j);
+        }
+    }
+    // the two scheduling barriers pin this issue order
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Gates (gdn_decode/solution/triton/kernel.py:123-131), computed while the state
+    // is in flight.
+    const float A_log = p.A_log[h * p.A_log_s];
+    const float dtb = p.dt_bias[h * p.dt_s];
+    const float x = bf16_to_f32(a_raw) + dtb;
+    const float sp = x > 20.f ? x : logf(1.f + expf(x));
+    const float alpha = expf(-expf(A_log) * sp);
+    const float beta = 1.f / (1.f + expf(-bf16_to_f32(b_raw)));
+
+    float kk[kCols], qq[kCols];
+#pragma unroll
+    for (int j = 0; j < kNV4; ++j) {
+        kk[4 * j + 0] = bf16lo(kraw[j].x);
+        kk[4 * j + 1] = bf16hi(kraw[j].x);
+        kk[4 * j + 2] = bf16lo(kraw[j].y);
+        kk[4 * j + 3] = bf16hi(kraw[j].y);
+        qq[4 * j + 0] = bf16lo(qraw[j].x);
+        qq[4 * j + 1] = bf16hi(qraw[j].x);
+        qq[4 * j + 2] = bf16lo(qraw[j].y);
+        qq[4 * j + 3] = bf16hi(qraw[j].y);
     }
     float vrow[RPT];
 #pragma unroll
     for (int r = 0; r < RPT; ++r)
-        vrow[r] = bf16_to_f32(p.v[bi * p.v_sb + h * p.v_sh + v0 + rg + kDecRowsPerPass * r]);
+        vrow[r] = bf16_to_f32(vraw[r]);
 
     float kq = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < kCols; ++i)
         kq = fmaf(kk[i], qq[i], kq);
-    kq = group8_sum(kq);
+    kq = row_sum<LPR>(kq);
 
     float *nbase = p.new_state + bi * p.ns_sb + h * p.ns_sh;
     bf16_t *obase = p.out + bi * p.o_sb + h * p.o_sh;
     const float omb = 1.f - beta;
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-        const int row = v0 + rg + kDecRowsPerPass * r;
+        const int row = v0 + rg + kRowsPerPass * r;
         float sk = 0.f, sq = 0.f;
         if constexpr (HAS_STATE) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < kNV4; ++j) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     sk = fmaf(S[r][j][e], kk[4 * j + e], sk);
                     sq = fmaf(S[r][j][e], qq[4 * j + e], sq);
                 }
             }
-            sk = group8_sum(sk);
-            sq = group8_sum(sq);
+            sk = row_sum<LPR>(sk);
+            sq = row_sum<LPR>(sq);
         }
         const float u = alpha * sk;                  // (alpha S) k      kernel.py:165-166
         const float nv = beta * vrow[r] + omb * u;   // kernel.py:167
@@ -155,14 +181,14 @@ __global__ __launch_bounds__(kDecThreads) void gdn_decode_kernel(DecodeArgs p)
         const float o = fmaf(alpha, sq, d * kq);     // (alpha S + d k^T) q
         float *nrow = nbase + (int64_t)row * p.ns_sv + 4 * s;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kNV4; ++j) {
             f32x4 w;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float sv = HAS_STATE ? S[r][j][e] : 0.f;
                 w[e] = fmaf(alpha, sv, d * kk[4 * j + e]);  // kernel.py:169
             }
-            st4<NT>(nrow + 32 * j, w);
+            st4<NT>(nrow + 4 * LPR * j, w);
         }
         if (s == 0)
             obase[row] = (bf16_t)f32_to_bf16(p.scale * o);  // kernel.py:216-218
@@ -175,20 +201,20 @@ namespace {
 
 using gdn::DecodeArgs;
 
-template <int RPT, bool NT>
-int launch_rpt(const DecodeArgs &a, int64_t nstates, hipStream_t stream)
+template <int THREADS, int LPR, int RPT, bool NT>
+int launch_cfg(const DecodeArgs &a, int64_t nstates, hipStream_t stream)
 {
-    constexpr int kNVT = gdn::kD / (gdn::kDecRowsPerPass * RPT);
+    constexpr int kNVT = gdn::kD / ((THREADS / LPR) * RPT);
     const int64_t blocks = (int64_t)nstates * kNVT;
     if (blocks > 0x7fffffff)
         return gdn_set_error(GDN_EINVAL, "gdn_decode: grid too large (%lld workgroups)",
                              (long long)blocks);
     if (a.state)
-        hipLaunchKernelGGL((gdn::gdn_decode_kernel<RPT, NT, true>), dim3((unsigned)blocks),
-                           dim3(gdn::kDecThreads), 0, stream, a);
+        hipLaunchKernelGGL((gdn::gdn_decode_kernel<THREADS, LPR, RPT, NT, true>),
+                           dim3((unsigned)blocks), dim3(THREADS), 0, stream, a);
     else
-        hipLaunchKernelGGL((gdn::gdn_decode_kernel<RPT, NT, false>), dim3((unsigned)blocks),
-                           dim3(gdn::kDecThreads), 0, stream, a);
+        hipLaunchKernelGGL((gdn::gdn_decode_kernel<THREADS, LPR, RPT, NT, false>),
+                           dim3((unsigned)blocks), dim3(THREADS), 0, stream, a);
     return gdn_check_launch("gdn_decode_kernel");
 }
 
@@ -274,15 +300,18 @@ extern "C" int gdn_decode_launch(const gdn_decode_params *p, void *stream)
 
     const int64_t nstates = (int64_t)B * HV;
     hipStream_t st = (hipStream_t)stream;
-    // variant: rows per thread x non-temporal hint. 0 (the default) = 1 row per thread,
-    // non-temporal: the fastest on MI355X at B = 1, 64 and 256.
+    // variant (tuning sweeps): workgroup size x lanes per state row x rows per lane
+    // x non-temporal hint; 0 is the default.
     switch (p->variant) {
-    case 1: return launch_rpt<2, true>(a, nstates, st);
-    case 2: return launch_rpt<4, true>(a, nstates, st);
-    case 3: return launch_rpt<1, false>(a, nstates, st);
-    case 4: return launch_rpt<2, false>(a, nstates, st);
-    case 5: return launch_rpt<4, false>(a, nstates, st);
-    default: return launch_rpt<1, true>(a, nstates, st);
+    case 1: return launch_cfg<256, 8, 2, true>(a, nstates, st);
+    case 2: return launch_cfg<256, 8, 4, true>(a, nstates, st);
+    case 3: return launch_cfg<256, 8, 1, false>(a, nstates, st);
+    case 4: return launch_cfg<256, 16, 1, true>(a, nstates, st);
+    case 5: return launch_cfg<128, 8, 1, true>(a, nstates, st);
+    case 6: return launch_cfg<128, 16, 1, true>(a, nstates, st);
+    case 7: return launch_cfg<256, 16, 2, true>(a, nstates, st);
+    case 8: return launch_cfg<64, 8, 1, true>(a, nstates, st);
+    default: return launch_cfg<256, 8, 1, true>(a, nstates, st);
     }
 
 }
