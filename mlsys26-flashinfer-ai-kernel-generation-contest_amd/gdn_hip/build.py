@@ -14,7 +14,9 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)  # the package root holding csrc/
 REPO = os.path.dirname(ROOT)
 CSRC = os.path.join(ROOT, "csrc")
-INCLUDE = os.path.join(REPO, "include")
+# the C ABI header: <repo>/include in the repository, <root>/include in a packed solution
+INCLUDE = next((d for d in (os.path.join(REPO, "include"), os.path.join(ROOT, "include"))
+                if os.path.exists(os.path.join(d, "gdn_hip.h"))), os.path.join(REPO, "include"))
 LIB_PATH = os.path.join(PKG_DIR, "libgdn_hip.so")
 ARCH = "gfx950"
 
