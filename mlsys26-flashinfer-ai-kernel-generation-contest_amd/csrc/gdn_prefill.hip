@@ -426,8 +426,12 @@ struct ChunkRegs {
     float gC;
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
-gdn_prefill_scan_kernel(ScanArgs p)
+// PREFETCH: the next chunk's operands are loaded into registers while the current
+// chunk computes (two register sets, 2 waves per SIMD). Otherwise each chunk's
+// loads are issued together at the start of its step (one set, more waves per SIMD
+// hide the latency instead).
+template <bool PREFETCH>
+__device__ __forceinline__ void scan_body(const ScanArgs &p)
 {
     // Workgroups of one (sequence, q/k head) group share K, Q, T and P through L2:
     // place them on one XCD (workgroup ids are dealt to the 8 XCDs round-robin).
@@ -549,8 +553,12 @@ gdn_prefill_scan_kernel(ScanArgs p)
 
     auto step = [&](ChunkRegs &cur, ChunkRegs &nxt, int c) {
         const int lenc = min(kC, len - c * kC);
-        if (c + 1 < nck)
-            load_chunk(nxt, c + 1);  // in flight while this chunk computes
+        if constexpr (PREFETCH) {
+            if (c + 1 < nck)
+                load_chunk(nxt, c + 1);  // in flight while this chunk computes
+        } else {
+            load_chunk(cur, c);
+        }
         // Q of this chunk: first needed by the readout (d), after three phases
         u32x4 qf[4];
         {
@@ -669,13 +677,19 @@ gdn_prefill_scan_kernel(ScanArgs p)
         stage_state();
     };
 
-    ChunkRegs ra, rb;
-    if (nck > 0)
-        load_chunk(ra, 0);
-    for (int c = 0; c < nck; c += 2) {
-        step(ra, rb, c);
-        if (c + 1 < nck)
-            step(rb, ra, c + 1);
+    if constexpr (PREFETCH) {
+        ChunkRegs ra, rb;
+        if (nck > 0)
+            load_chunk(ra, 0);
+        for (int c = 0; c < nck; c += 2) {
+            step(ra, rb, c);
+            if (c + 1 < nck)
+                step(rb, ra, c + 1);
+        }
+    } else {
+        ChunkRegs r;
+        for (int c = 0; c < nck; ++c)
+            step(r, r, c);
     }
 
 #pragma unroll
@@ -685,6 +699,24 @@ gdn_prefill_scan_kernel(ScanArgs p)
             const int vv = v0 + 4 * lg + i, kc = 16 * (2 * w + j) + lr;
             p.new_state[n * p.ns_sn + h * p.ns_sh + vv * p.ns_sv + kc] = Sreg[j][i];
         }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gdn_prefill_scan_kernel(ScanArgs p)
+{
+    scan_body<true>(p);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void
+gdn_prefill_scan_kernel_nopf3(ScanArgs p)
+{
+    scan_body<false>(p);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void
+gdn_prefill_scan_kernel_nopf4(ScanArgs p)
+{
+    scan_body<false>(p);
 }
 
 }  // namespace gdn
@@ -893,8 +925,18 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         const int64_t blocks = 8 * (8 * (int64_t)ratio) * ((ngroups + 7) / 8);
         if (ngroups > 0x7fffffff || blocks > 0x7fffffff)
             return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
-        hipLaunchKernelGGL(gdn::gdn_prefill_scan_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                           sa);
+        // variant (tuning sweeps): 0 = per-chunk batched loads at 3 waves per SIMD (the
+        // fastest on MI355X), 1 = next-chunk register prefetch at 2 waves per SIMD,
+        // 2 = batched loads at 4 waves per SIMD
+        if (p->variant == 1)
+            hipLaunchKernelGGL(gdn::gdn_prefill_scan_kernel, dim3((unsigned)blocks), dim3(256),
+                               0, st, sa);
+        else if (p->variant == 2)
+            hipLaunchKernelGGL(gdn::gdn_prefill_scan_kernel_nopf4, dim3((unsigned)blocks),
+                               dim3(256), 0, st, sa);
+        else
+            hipLaunchKernelGGL(gdn::gdn_prefill_scan_kernel_nopf3, dim3((unsigned)blocks),
+                               dim3(256), 0, st, sa);
         rc = gdn_check_launch("gdn_prefill_scan_kernel");
         if (rc)
             return rc;

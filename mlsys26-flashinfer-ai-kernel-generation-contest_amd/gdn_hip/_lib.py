@@ -66,6 +66,8 @@ class PrefillParams(ctypes.Structure):
         ("head_size", _c_i32),
         ("scale", _c_f32),
         ("cu_seqlens_int64", _c_i32),
+        ("variant", _c_i32),
+        ("reserved", _c_i32),
         ("q", _c_ptr), ("q_stride", _c_i64 * 3),
         ("k", _c_ptr), ("k_stride", _c_i64 * 3),
         ("v", _c_ptr), ("v_stride", _c_i64 * 3),

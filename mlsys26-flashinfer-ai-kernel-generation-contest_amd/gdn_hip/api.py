@@ -235,6 +235,15 @@ def set_decode_variant(v: int) -> None:
 
 
 # ----------------------------------------------------------------------------- prefill
+_prefill_variant = 0
+
+
+def set_prefill_variant(v: int) -> None:
+    """Select a prefill kernel variant (tuning sweeps; 0 = tuned default)."""
+    global _prefill_variant
+    _prefill_variant = int(v)
+
+
 _ws_lock = threading.Lock()
 _ws_cache: dict = {}
 
@@ -341,6 +350,7 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=
     P.total_tokens, P.num_seqs, P.num_qk_heads, P.num_v_heads, P.head_size = T, N, HQK, HV, D
     P.scale = scale
     P.cu_seqlens_int64 = 1 if cu_.dtype == torch.int64 else 0
+    P.variant = _prefill_variant
     P.q, P.q_stride = _ptr(q_), _strides(q_, 3)
     P.k, P.k_stride = _ptr(k_), _strides(k_, 3)
     P.v, P.v_stride = _ptr(v_), _strides(v_, 3)
