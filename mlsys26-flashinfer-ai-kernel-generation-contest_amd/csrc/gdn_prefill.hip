@@ -49,10 +49,11 @@ constexpr int kLdT = 72;  // padded LDS row (bf16) for 16 x 64 tiles
 // stored as their 10 lower 16x16 blocks, block (i, j <= i) at index i(i+1)/2 + j,
 // each block row-major: exactly the rows and 8-column runs an MFMA A operand reads.
 constexpr int kBlk = 256;        // elements per 16x16 block
-constexpr int kRecThi = 0;       // bf16 [10][16][16]  T = (I + A)^-1, high half
+// Byte offsets:
+constexpr int kRecThi = 0;       // bf16 [10][16][16]  T' = (I + A)^-1 diag(beta), high half
 constexpr int kRecTlo = 5120;    // bf16 [10][16][16]  low half
-constexpr int kRecP = 10240;     // bf16 [10][16][16]  P (decayed, causal Q K^T)
-constexpr int kRecGates = 15360; // f32 beta[64], gamma[64], dec[64], gammaC
+constexpr int kRecP = 10240;     // bf16 [10][16][16]  P' = scale * P (decayed, causal Q K^T)
+constexpr int kRecGates = 15360; // f32 gamma[64], dec[64], scale * gamma[64], gammaC
 constexpr int kRecZero = 16256;  // 16 zero bytes (after the gates): what absent blocks read
 constexpr int kRecBytes = 16384;
 
@@ -188,6 +189,7 @@ struct PrepArgs {
     const int32_t *header, *chunk_tok0, *chunk_len;
     char *records;
     int HQK, HV, ratio;
+    float scale;
 };
 
 // Lower-triangular 16x16 tile t of a 64x64 matrix -> (row block, column block).
@@ -282,9 +284,10 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
         Lg[l] = L;
         Bt[l] = bt;
         float *gates = (float *)(rec + kRecGates);
-        gates[l] = bt;
-        gates[64 + l] = __builtin_amdgcn_exp2f(L);
-        gates[128 + l] = __builtin_amdgcn_exp2f(Lend - L);
+        const float gam = __builtin_amdgcn_exp2f(L);
+        gates[l] = gam;
+        gates[64 + l] = __builtin_amdgcn_exp2f(Lend - L);
+        gates[128 + l] = p.scale * gam;
         if (l == 0)
             gates[192] = __builtin_amdgcn_exp2f(Lend);
         if (l < 4)
@@ -309,11 +312,12 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
             r = mfma_bf16(a, bk, r);
         }
         acc[m] = r;
-        if (isq) {  // P = exp(L_t - L_j) q_t . k_j for j <= t, bf16, block layout
+        if (isq) {  // P' = scale exp(L_t - L_j) q_t . k_j for j <= t, bf16, block layout
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int tt = 16 * ti + 4 * lg + e, jj = 16 * tj + lr;
-                const float pv = jj <= tt ? __builtin_amdgcn_exp2f(Lg[tt] - Lg[jj]) * r[e] : 0.f;
+                const float pv =
+                    jj <= tt ? p.scale * __builtin_amdgcn_exp2f(Lg[tt] - Lg[jj]) * r[e] : 0.f;
                 Ps[t * kBlk + (4 * lg + e) * 16 + lr] = (bf16_t)f32_to_bf16(pv);
             }
         }
@@ -388,15 +392,18 @@ __global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
         lds_barrier();
     }
 
-    // T -> record (bf16 hi / lo, block layout); 16-byte pieces.
+    // T' = T diag(beta) -> record (bf16 hi / lo, block layout); 16-byte pieces. Padding
+    // tokens have beta = 0, so their columns of T' are zero.
     for (int q = tid; q < 10 * kBlk / 8; q += 256) {
         const int bidx = q >> 5, row = (q & 31) >> 1, c8 = (q & 1) * 8;
         const int bi = tile_i(bidx), bj = tile_j(bidx);
         uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            split_bf16x2(Ts[16 * bi + row][16 * bj + c8 + 2 * e],
-                         Ts[16 * bi + row][16 * bj + c8 + 2 * e + 1], hw[e], lw[e]);
+        for (int e = 0; e < 4; ++e) {
+            const int j0 = 16 * bj + c8 + 2 * e;
+            split_bf16x2(Ts[16 * bi + row][j0] * Bt[j0], Ts[16 * bi + row][j0 + 1] * Bt[j0 + 1],
+                         hw[e], lw[e]);
+        }
         *(u32x4 *)(rec + kRecThi + q * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
         *(u32x4 *)(rec + kRecTlo + q * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
     }
@@ -413,310 +420,337 @@ struct ScanArgs {
     const int32_t *header, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
     const char *records;
     int HQK, HV, ratio, ngroups;
-    float scale;
 };
 
-// One chunk's operands for one lane, loaded a chunk ahead (MFMA A-operand layouts).
-struct ChunkRegs {
-    u32x4 kf[4];         // K rows 16w+lr, columns 32ks + 8lg .. +7
-    u32x4 th[2], tl[2];  // T hi / lo rows 16w+lr, columns 32ks + 8lg .. +7
-    u32x4 pf[2];         // P, same layout as T
-    uint32_t vv[4];      // V[16w + 4lg + i][v0 + lr] (bf16 bits)
-    f32x4 beta, gamma, dec;  // gates of tokens 16w + 4lg + 0..3
-    float gC;
-};
+#define GDN_LDS __attribute__((address_space(3)))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-// PREFETCH: the next chunk's operands are loaded into registers while the current
-// chunk computes (two register sets, 2 waves per SIMD). Otherwise each chunk's
-// loads are issued together at the start of its step (one set, more waves per SIMD
-// hide the latency instead).
-template <bool PREFETCH>
-__device__ __forceinline__ void scan_body(const ScanArgs &p)
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i writes
+// dst + 16 i; dst is wave-uniform, src is per lane.
+__device__ __forceinline__ void dma16(const char *src, void *dst)
 {
-    // Workgroups of one (sequence, q/k head) group share K, Q, T and P through L2:
-    // place them on one XCD (workgroup ids are dealt to the 8 XCDs round-robin).
+    __builtin_amdgcn_global_load_lds((const void *)src, (GDN_LDS void *)dst, 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane n receives element n % 4 of the
+// four 8-byte pieces addressed by lanes n / 4 + 4 r, r = 0..3 (element r of the result).
+__device__ __forceinline__ u32x2 lds_tr16(const void *p)
+{
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GDN_LDS s16x4 *)p);
+    return __builtin_bit_cast(u32x2, r);
+}
+
+// Wait for this wave's LDS copies, then for the whole workgroup.
+__device__ __forceinline__ void dma_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    lds_barrier();
+}
+
+// Bank swizzles (16-byte units; every operand read below covers 16 distinct bank groups):
+//   K row t, k-chunk c (k = 8c .. 8c+7)   -> unit 16 t + (c ^ kswz(t))
+//   Q row t, k-chunk c                    -> unit 16 t + (c ^ (t & 15))
+//   V row t, v-chunk c                    -> unit 2 NW t + (c ^ 2 (t & 3))
+//   T' / P' block (i, j), row r, half h    -> unit 32 (4 i + j) + (bswz(r, h) ^ 8 (i & 1))
+__device__ __forceinline__ int kswz(int t) { return ((t & 3) << 2) | ((t >> 3) & 3); }
+__device__ __forceinline__ int bswz(int r, int h) { return 2 * r + (h ^ (r >> 3)); }
+
+// One chunk in LDS, as the workgroup's waves read it.
+template <int NW>
+struct ScanBuf {
+    u32x4 K[kC * 16];      // 16 KB
+    u32x4 Q[kC * 16];      // 16 KB
+    u32x4 V[kC * 2 * NW];  // the workgroup's 16 NW value columns
+    u32x4 T[2][16 * 32];   // T' hi / lo as 4 x 4 dense 16x16 blocks
+    u32x4 P[16 * 32];      // P' blocks
+    f32x4 G[64];           // the record's gate area (gamma, dec, scale gamma, gammaC)
+};
+
+// Copy windows of one chunk, 64 units (1 KB) each: K rows 4b..4b+3 (16 windows), Q (16),
+// V (NW == 8: 4 rows per window, NW == 4: 8 rows), then 18 T' / P' block pairs and the
+// gate area. Record windows read block pairs {(i, j), (i, j + 1)} of the dense layout
+// starting at blocks 0, 4, 8, 10, 12, 14; blocks above the diagonal read the record's
+// zero bytes.
+
+// Workgroup: NW waves, each owning 16 state rows v0 + 16 w .. of one (sequence, v-head)
+// for all 128 columns; the waves share the chunk's K, Q, V, T', P' through LDS and
+// never exchange state. Per chunk and wave (state S0 at chunk start, T' = T diag(beta)):
+//   X  = K S0^T                      (S0 as bf16 hi + lo)
+//   R  = V - gamma X
+//   U  = T' R                        (T', R as hi + lo; three products)
+//   O  = scale gamma Q S0^T + P' U   (S0 hi, U bf16)
+//   S  = gammaC S0 + (dec U)^T K     (dec U as hi + lo)
+// Row orders inside a 32-row block are permuted so that every MFMA result is already
+// the next MFMA's operand: X and U tiles use token rows 32 (tt/2) + 8 (m/4) + 4 (tt%2)
+// + m%4, state tiles kt = 2s + h hold columns 32 s + 8 (m/4) + 4 h + m%4. K^T and the
+// V columns are read with the LDS transpose read.
+template <int NW>
+__device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, ScanBuf<NW> &BB)
+{
+    constexpr int TPH = 8 / NW;  // workgroups per (sequence, v-head)
+    // Workgroups of one (sequence, q/k head) share K, Q through L2: one XCD for them all
+    // (workgroup ids are dealt to the 8 XCDs round-robin).
     const int pid = blockIdx.x, xcd = pid & 7, slot = pid >> 3;
-    const int gsz = 8 * p.ratio;
+    const int gsz = TPH * p.ratio;
     const int wi = slot % gsz;
     const int grp = (slot / gsz) * 8 + xcd;
     if (grp >= p.ngroups)
         return;
     const int n = p.seq_order[grp / p.HQK];
     const int g = grp % p.HQK;
-    const int h = g * p.ratio + wi / 8;
-    const int v0 = (wi % 8) * 16;
+    const int h = g * p.ratio + wi / TPH;
+    const int v0 = (wi % TPH) * 16 * NW;
     const int tok0 = p.seq_tok0[n], len = p.seq_len[n], c0 = p.seq_chunk0[n];
     // records exist only for chunk ids < header[0] (see the plan kernel's clamp)
     const int nck = min((len + kC - 1) / kC, max(p.header[0] - c0, 0));
 
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
+    const int v0w = v0 + 16 * w;
 
-    __shared__ __align__(16) bf16_t Ks[kC][kLdK];
-    __shared__ __align__(16) bf16_t Shi[16][kLdK];
-    __shared__ __align__(16) bf16_t Slo[16][kLdK];
-    __shared__ __align__(16) bf16_t RThi[16][kLdT];
-    __shared__ __align__(16) bf16_t RTlo[16][kLdT];
-    __shared__ __align__(16) bf16_t UThi[16][kLdT];
-    __shared__ __align__(16) bf16_t WThi[16][kLdT];
-    __shared__ __align__(16) bf16_t WTlo[16][kLdT];
-
-    // Addressing: per chunk a wave-uniform 64-bit base (scalar registers) plus a 32-bit
-    // per-lane byte offset (the host keeps token / head strides below 2^24 elements),
-    // so loads and stores use the scalar-base + vector-offset form.
-    const int trow = 16 * w + lr;             // token row of this lane's A operands
-    const int tcol = 16 * w + 4 * lg;         // first of this lane's 4 C-layout token rows
+    // ---- copy plan (per lane; chunk-invariant parts)
     const uint32_t kst2 = (uint32_t)p.k_st * 2, qst2 = (uint32_t)p.q_st * 2;
     const uint32_t vst2 = (uint32_t)p.v_st * 2, ost2 = (uint32_t)p.o_st * 2;
     const char *kbase = (const char *)(p.k + (int64_t)tok0 * p.k_st + g * p.k_sh);
     const char *qbase = (const char *)(p.q + (int64_t)tok0 * p.q_st + g * p.q_sh);
-    const char *vbase = (const char *)(p.v + (int64_t)tok0 * p.v_st + h * p.v_sh);
-    char *obase = (char *)(p.out + (int64_t)tok0 * p.o_st + h * p.o_sh);
+    const char *vbase = (const char *)(p.v + (int64_t)tok0 * p.v_st + h * p.v_sh + v0);
+    char *obase = (char *)(p.out + (int64_t)tok0 * p.o_st + h * p.o_sh + v0w);
     const int64_t kstep = (int64_t)kC * p.k_st * 2, qstep = (int64_t)kC * p.q_st * 2;
     const int64_t vstep = (int64_t)kC * p.v_st * 2, ostep = (int64_t)kC * p.o_st * 2;
     const char *rbase = p.records + ((int64_t)c0 * p.HV + h) * kRecBytes;
     const int64_t rstep = (int64_t)p.HV * kRecBytes;
-    // Byte offsets of this lane's T / P A-operand pieces inside a record; blocks above
-    // the diagonal are not stored and read the record's zero bytes instead.
-    uint32_t thoff[2], tloff[2], poff[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int jb = 2 * ks + (lg >> 1);
-        const uint32_t o = 2u * (tri_blk(w, jb) * kBlk + lr * 16 + 8 * (lg & 1));
-        thoff[ks] = jb <= w ? kRecThi + o : kRecZero;
-        tloff[ks] = jb <= w ? kRecTlo + o : kRecZero;
-        poff[ks] = jb <= w ? kRecP + o : kRecZero;
-    }
-    const uint32_t lane_col = 16u * lg;                 // 8 bf16 per lane group
-    const uint32_t v_col = 2u * (v0 + lr);
-    const uint32_t o_col = 2u * (v0 + (lr & ~1));
-    const uint32_t g_off = 4u * tcol;
 
-    // Rows past a chunk's end are clamped to its last token instead of zeroed: they
-    // carry beta = 0 and decay weight 0, so they contribute exactly nothing, and their
-    // outputs are not stored. Every load reads valid memory and stays in flight.
-    auto load_chunk = [&](ChunkRegs &r, int c) {
+    constexpr int VWIN = 2 * NW;               // V windows
+    constexpr int NWIN = 32 + VWIN + 19;       // all windows
+    constexpr int PER = (NWIN + NW - 1) / NW;  // windows per wave
+
+    auto issue_chunk = [&](ScanBuf<NW> &B, int c) {
         const int lenc = min(kC, len - c * kC);
-        const char *rec = rbase + c * rstep;
-        const char *kc_ = kbase + c * kstep;
-        const uint32_t ko = (uint32_t)min(trow, lenc - 1) * kst2 + lane_col;
+        const char *kc_ = kbase + c * kstep, *qc_ = qbase + c * qstep, *vc_ = vbase + c * vstep;
+        const char *rc_ = rbase + c * rstep;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            r.kf[ks] = *(const u32x4 *)(kc_ + ko + 64 * ks);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            r.th[ks] = *(const u32x4 *)(rec + thoff[ks]);
-            r.tl[ks] = *(const u32x4 *)(rec + tloff[ks]);
-            r.pf[ks] = *(const u32x4 *)(rec + poff[ks]);
-        }
-        const char *vc_ = vbase + c * vstep;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            r.vv[i] = *(const bf16_t *)(vc_ + (uint32_t)min(tcol + i, lenc - 1) * vst2 + v_col);
-        const char *gt = rec + kRecGates;
-        r.beta = *(const f32x4 *)(gt + g_off);
-        r.gamma = *(const f32x4 *)(gt + 256 + g_off);
-        r.dec = *(const f32x4 *)(gt + 512 + g_off);
-        r.gC = *(const float *)(gt + 768);
-    };
-
-    // State tile rows v0..v0+15 in MFMA C layout: Sreg[j][i] = S[v0 + 4 lg + i][16 (2w + j) + lr].
-    f32x4 Sreg[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int vv = v0 + 4 * lg + i, kc = 16 * (2 * w + j) + lr;
-            Sreg[j][i] = p.state ? p.state[n * p.st_sn + h * p.st_sh + vv * p.st_sv + kc] : 0.f;
-        }
-    // S -> LDS as bf16 hi / lo. Lanes lr and lr^1 hold neighbouring columns: even lanes
-    // store rows 0,1 and odd lanes rows 2,3 of the pair as packed 32-bit words (element
-    // indices stay static: the lane choice only predicates the stores).
-    const bool even = (lr & 1) == 0;
-    auto stage_state = [&]() {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = (16 * (2 * w + j) + lr) & ~1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float mine = Sreg[j][i];
-                const float oth = dpp_mov<kDppQuadXor1>(mine);
-                uint32_t hi, lo;
-                split_bf16x2(even ? mine : oth, even ? oth : mine, hi, lo);
-                if (even == (i < 2)) {
-                    *(uint32_t *)&Shi[4 * lg + i][col] = hi;
-                    *(uint32_t *)&Slo[4 * lg + i][col] = lo;
+        for (int i = 0; i < PER; ++i) {
+            const int win = w + NW * i;  // window kind is a compile-time function of i
+            if (NW * i < 16) {
+                const int t = 4 * win + (l >> 4), cs = l & 15;
+                const uint32_t off = (uint32_t)min(t, lenc - 1) * kst2 + 16u * (cs ^ kswz(t));
+                dma16(kc_ + off, &B.K[64 * win]);
+            } else if (NW * i < 32) {
+                const int b = win - 16, t = 4 * b + (l >> 4), cs = l & 15;
+                const uint32_t off = (uint32_t)min(t, lenc - 1) * qst2 + 16u * (cs ^ (t & 15));
+                dma16(qc_ + off, &B.Q[64 * b]);
+            } else if (NW * i < 32 + VWIN) {
+                const int b = win - 32;
+                const int t = NW == 8 ? 4 * b + (l >> 4) : 8 * b + (l >> 3);
+                const int cs = NW == 8 ? (l & 15) : (l & 7);
+                const uint32_t off = (uint32_t)min(t, lenc - 1) * vst2 + 16u * (cs ^ (2 * (t & 3)));
+                dma16(vc_ + off, &B.V[64 * b]);
+            } else if (win < NWIN) {
+                const int r = win - 32 - VWIN;
+                if (r < 18) {
+                    const int mt = r / 6, pr = r % 6, d0 = pr < 3 ? 4 * pr : 2 * pr + 4;
+                    const int d = d0 + (l >> 5), bi = d >> 2, bj = d & 3;
+                    const int u = (l & 31) ^ (8 * (bi & 1)), rho = u >> 1, hf = (u & 1) ^ (rho >> 3);
+                    const int mbase = mt == 0 ? kRecThi : (mt == 1 ? kRecTlo : kRecP);
+                    const uint32_t off = bj <= bi
+                        ? (uint32_t)(mbase + (tri_blk(bi, bj) * 32 + 2 * rho + hf) * 16)
+                        : (uint32_t)kRecZero;
+                    u32x4 *dst = mt == 2 ? &B.P[32 * d0] : &B.T[mt][32 * d0];
+                    dma16(rc_ + off, dst);
+                } else {
+                    dma16(rc_ + kRecGates + 16 * l, &B.G[0]);
                 }
             }
         }
     };
-    stage_state();
 
-    auto step = [&](ChunkRegs &cur, ChunkRegs &nxt, int c) {
+    // ---- LDS read offsets (bytes within a ScanBuf member; chunk-invariant)
+    const int c_ = lr & 3, r_ = lr >> 2;
+    uint32_t koffA[4], ktoff[4], qoff[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        koffA[s] = 16u * (16 * (8 * (lr >> 2) + (lr & 3)) + (((s ^ (lr & 3)) << 2) | (lg ^ (lr >> 2))));
+        ktoff[s] = 256u * (8 * lg + r_) + 16u * (((s ^ r_) << 2) | (c_ ^ lg));
+        qoff[s] = 16u * (16 * lr + ((4 * s + lg) ^ lr));
+    }
+    const uint32_t voff = 32u * NW * (8 * lg + r_) + 16u * ((2 * w + (c_ >> 1)) ^ (2 * r_)) + 8u * (c_ & 1);
+    const int mu = lr >> 3, a_ = (lr >> 2) & 1, lam = lg >> 1, hf = lg & 1;
+    uint32_t toff[2], poff[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        toff[b] = 512u * (4 * mu + lam) + 16u * ((16 * a_ + 8 * b + 2 * (lr & 3) + (hf ^ a_)) ^ (8 * mu));
+        poff[b] = 512u * lam + 16u * (bswz(lr, hf) ^ (8 * b));
+    }
+    const uint32_t goff = 32u * lg, sgoff = 4u * lr;
+
+    // ---- state: S[2 s + h] holds S[v0w + lr][32 s + 8 lg + 4 h + i], i = 0..3
+    if (nck > 0)
+        issue_chunk(BA, 0);
+    f32x4 S[8];
+    {
+        const float *sp = p.state ? p.state + n * p.st_sn + h * p.st_sh + (int64_t)(v0w + lr) * p.st_sv + 8 * lg
+                                  : nullptr;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            S[2 * s] = sp ? *(const f32x4 *)(sp + 32 * s) : f32x4{0.f, 0.f, 0.f, 0.f};
+            S[2 * s + 1] = sp ? *(const f32x4 *)(sp + 32 * s + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    auto compute = [&](ScanBuf<NW> &B, int c) {
         const int lenc = min(kC, len - c * kC);
-        if constexpr (PREFETCH) {
-            if (c + 1 < nck)
-                load_chunk(nxt, c + 1);  // in flight while this chunk computes
-        } else {
-            load_chunk(cur, c);
-        }
-        // Q of this chunk: first needed by the readout (d), after three phases
-        u32x4 qf[4];
-        {
-            const char *qc_ = qbase + c * qstep;
-            const uint32_t qo = (uint32_t)min(trow, lenc - 1) * qst2 + lane_col;
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                qf[ks] = *(const u32x4 *)(qc_ + qo + 64 * ks);
-        }
+        const char *Kb = (const char *)B.K, *Qb = (const char *)B.Q, *Vb = (const char *)B.V;
+        const char *Th = (const char *)B.T[0], *Tl = (const char *)B.T[1];
+        const char *Pb = (const char *)B.P, *Gb = (const char *)B.G;
 
-        // K rows of this wave -> LDS (the state update reads K by columns)
+        // (a) S0 as MFMA operands (hi + lo), X = K S0^T
+        u32x4 Bh[4], Bl[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            *(u32x4 *)&Ks[trow][ks * 32 + 8 * lg] = cur.kf[ks];
-        lds_barrier();
-
-        // (a) X = K S0^T for tokens 16w..16w+15 (S0 as hi + lo; two accumulators keep
-        // the dependent MFMA chains short)
-        f32x4 X = {0.f, 0.f, 0.f, 0.f}, Xl = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const u32x4 bh = *(const u32x4 *)&Shi[lr][ks * 32 + 8 * lg];
-            const u32x4 bl = *(const u32x4 *)&Slo[lr][ks * 32 + 8 * lg];
-            X = mfma_bf16(cur.kf[ks], bh, X);
-            Xl = mfma_bf16(cur.kf[ks], bl, Xl);
+        for (int s = 0; s < 4; ++s) {
+            uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+            split_bf16x2(S[2 * s][0], S[2 * s][1], h0, l0);
+            split_bf16x2(S[2 * s][2], S[2 * s][3], h1, l1);
+            split_bf16x2(S[2 * s + 1][0], S[2 * s + 1][1], h2, l2);
+            split_bf16x2(S[2 * s + 1][2], S[2 * s + 1][3], h3, l3);
+            Bh[s] = u32x4{h0, h1, h2, h3};
+            Bl[s] = u32x4{l0, l1, l2, l3};
         }
-        X += Xl;
-        // (b) R = beta (V - gamma X) -> LDS as R^T (hi, lo)
-        {
-            float r[4];
+        f32x4 X[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                r[i] = cur.beta[i] * (bf16_to_f32(cur.vv[i]) - cur.gamma[i] * X[i]);
+        for (int tt = 0; tt < 4; ++tt)
+            X[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const u32x4 a = *(const u32x4 *)(Kb + koffA[s] + 256 * (32 * (tt >> 1) + 4 * (tt & 1)));
+                X[tt] = mfma_bf16(a, Bh[s], X[tt]);
+                X[tt] = mfma_bf16(a, Bl[s], X[tt]);
+            }
+
+        // (b) R = V - gamma X -> operands (hi + lo) over token blocks s'
+        u32x4 Rh[2], Rl[2];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const int trow = 32 * (tt >> 1) + 4 * (tt & 1);
+            const u32x2 vv = lds_tr16(Vb + voff + 32 * NW * trow);
+            const f32x4 gm = *(const f32x4 *)(Gb + goff + 4 * trow);
+            const float r0 = fmaf(-gm[0], X[tt][0], bf16lo(vv[0]));
+            const float r1 = fmaf(-gm[1], X[tt][1], bf16hi(vv[0]));
+            const float r2 = fmaf(-gm[2], X[tt][2], bf16lo(vv[1]));
+            const float r3 = fmaf(-gm[3], X[tt][3], bf16hi(vv[1]));
             uint32_t h01, l01, h23, l23;
-            split_bf16x2(r[0], r[1], h01, l01);
-            split_bf16x2(r[2], r[3], h23, l23);
-            *(u32x2 *)&RThi[lr][tcol] = u32x2{h01, h23};
-            *(u32x2 *)&RTlo[lr][tcol] = u32x2{l01, l23};
+            split_bf16x2(r0, r1, h01, l01);
+            split_bf16x2(r2, r3, h23, l23);
+            if (tt & 1) {
+                Rh[tt >> 1][2] = h01; Rh[tt >> 1][3] = h23;
+                Rl[tt >> 1][2] = l01; Rl[tt >> 1][3] = l23;
+            } else {
+                Rh[tt >> 1][0] = h01; Rh[tt >> 1][1] = h23;
+                Rl[tt >> 1][0] = l01; Rl[tt >> 1][1] = l23;
+            }
         }
-        lds_barrier();
 
-        // (c) U = T R  (T, R as hi + lo; three products). Rows < 32 of T have no
-        // entries in columns >= 32.
-        f32x4 U = {0.f, 0.f, 0.f, 0.f}, Ul = {0.f, 0.f, 0.f, 0.f};
+        // (c) U = T' R
+        f32x4 U[4];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            if (ks == 1 && w < 2)
-                continue;
-            const u32x4 bh = *(const u32x4 *)&RThi[lr][ks * 32 + 8 * lg];
-            const u32x4 bl = *(const u32x4 *)&RTlo[lr][ks * 32 + 8 * lg];
-            U = mfma_bf16(cur.th[ks], bh, U);
-            Ul = mfma_bf16(cur.th[ks], bl, Ul);
-            Ul = mfma_bf16(cur.tl[ks], bh, Ul);
+        for (int tt = 0; tt < 4; ++tt) {
+            U[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sp = 0; sp <= (tt >> 1); ++sp) {
+                const uint32_t o = toff[tt & 1] + 512 * (8 * (tt >> 1) + 2 * sp);
+                const u32x4 th = *(const u32x4 *)(Th + o);
+                const u32x4 tl = *(const u32x4 *)(Tl + o);
+                U[tt] = mfma_bf16(th, Rh[sp], U[tt]);
+                U[tt] = mfma_bf16(th, Rl[sp], U[tt]);
+                U[tt] = mfma_bf16(tl, Rh[sp], U[tt]);
+            }
         }
-        U += Ul;
-        {
-            uint32_t wh01, wl01, wh23, wl23;
-            split_bf16x2(cur.dec[0] * U[0], cur.dec[1] * U[1], wh01, wl01);
-            split_bf16x2(cur.dec[2] * U[2], cur.dec[3] * U[3], wh23, wl23);
-            *(u32x2 *)&UThi[lr][tcol] = u32x2{pack_bf16x2(U[0], U[1]), pack_bf16x2(U[2], U[3])};
-            *(u32x2 *)&WThi[lr][tcol] = u32x2{wh01, wh23};
-            *(u32x2 *)&WTlo[lr][tcol] = u32x2{wl01, wl23};
-        }
-        lds_barrier();
 
-        // (d) O = scale (gamma Q S0^T + P U) for tokens 16w..16w+15
-        {
+        // (d) W = dec U (hi + lo) for the state update, U (bf16) for the readout
+        u32x4 Wh[2], Wl[2], Ub[2];
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const int trow = 32 * (tt >> 1) + 4 * (tt & 1);
+            const f32x4 dc = *(const f32x4 *)(Gb + 256 + goff + 4 * trow);
+            uint32_t h01, l01, h23, l23;
+            split_bf16x2(dc[0] * U[tt][0], dc[1] * U[tt][1], h01, l01);
+            split_bf16x2(dc[2] * U[tt][2], dc[3] * U[tt][3], h23, l23);
+            const uint32_t u01 = pack_bf16x2(U[tt][0], U[tt][1]), u23 = pack_bf16x2(U[tt][2], U[tt][3]);
+            const int e = 2 * (tt & 1);
+            Wh[tt >> 1][e] = h01; Wh[tt >> 1][e + 1] = h23;
+            Wl[tt >> 1][e] = l01; Wl[tt >> 1][e + 1] = l23;
+            Ub[tt >> 1][e] = u01; Ub[tt >> 1][e + 1] = u23;
+        }
+
+        // (e) O^T = scale gamma S0 Q^T + U^T P'^T; lane (t = 16 tt + lr) stores 4 values
+        char *oc_ = obase + c * ostep;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
             f32x4 Oi = {0.f, 0.f, 0.f, 0.f}, Oa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                Oi = mfma_bf16(qf[ks], *(const u32x4 *)&Shi[lr][ks * 32 + 8 * lg], Oi);
+            for (int s = 0; s < 4; ++s)
+                Oi = mfma_bf16(Bh[s], *(const u32x4 *)(Qb + qoff[s] + 4096 * tt), Oi);
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                if (ks == 1 && w < 2)
-                    continue;
-                Oa = mfma_bf16(cur.pf[ks], *(const u32x4 *)&UThi[lr][ks * 32 + 8 * lg], Oa);
-            }
-            // lanes lr, lr^1 pack neighbouring columns: even lanes store rows 0,1, odd 2,3
-            char *oc_ = obase + c * ostep;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float mine = p.scale * fmaf(cur.gamma[i], Oi[i], Oa[i]);
-                const float oth = dpp_mov<kDppQuadXor1>(mine);
-                const uint32_t packed = pack_bf16x2(even ? mine : oth, even ? oth : mine);
-                if (even == (i < 2) && tcol + i < lenc)
-                    *(uint32_t *)(oc_ + (uint32_t)(tcol + i) * ost2 + o_col) = packed;
-            }
+            for (int sp = 0; sp <= (tt >> 1); ++sp)
+                Oa = mfma_bf16(Ub[sp], *(const u32x4 *)(Pb + poff[tt & 1] + 512 * (4 * tt + 2 * sp)), Oa);
+            const float sg = *(const float *)(Gb + 512 + sgoff + 64 * tt);
+            const uint32_t o01 = pack_bf16x2(fmaf(sg, Oi[0], Oa[0]), fmaf(sg, Oi[1], Oa[1]));
+            const uint32_t o23 = pack_bf16x2(fmaf(sg, Oi[2], Oa[2]), fmaf(sg, Oi[3], Oa[3]));
+            const int t = 16 * tt + lr;
+            if (t < lenc)
+                *(u32x2 *)(oc_ + (uint32_t)t * ost2 + 8u * lg) = u32x2{o01, o23};
         }
 
-        // (e) S = gammaC S + W^T K over this wave's 32 state columns
+        // (f) S = gammaC S0 + W^T K
+        const float gC = *(const float *)(Gb + 768);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int kc = 16 * (2 * w + j) + lr;
-            f32x4 dS = {0.f, 0.f, 0.f, 0.f}, dSl = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const u32x4 awh = *(const u32x4 *)&WThi[lr][ks * 32 + 8 * lg];
-                const u32x4 awl = *(const u32x4 *)&WTlo[lr][ks * 32 + 8 * lg];
-                uint32_t kw[4];
+            for (int hh = 0; hh < 2; ++hh) {
+                f32x4 acc = gC * S[2 * s + hh];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t k0 = Ks[ks * 32 + 8 * lg + 2 * e][kc];
-                    const uint32_t k1 = Ks[ks * 32 + 8 * lg + 2 * e + 1][kc];
-                    kw[e] = k0 | (k1 << 16);
+                for (int sp = 0; sp < 2; ++sp) {
+                    const u32x2 k0 = lds_tr16(Kb + ktoff[s] + 256 * (32 * sp) + 8 * hh);
+                    const u32x2 k1 = lds_tr16(Kb + ktoff[s] + 256 * (32 * sp + 4) + 8 * hh);
+                    const u32x4 a = {k0[0], k0[1], k1[0], k1[1]};
+                    acc = mfma_bf16(a, Wh[sp], acc);
+                    acc = mfma_bf16(a, Wl[sp], acc);
                 }
-                const u32x4 bk = {kw[0], kw[1], kw[2], kw[3]};
-                dS = mfma_bf16(awh, bk, dS);
-                dSl = mfma_bf16(awl, bk, dSl);
+                S[2 * s + hh] = acc;
             }
-            dS += dSl;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                Sreg[j][i] = fmaf(cur.gC, Sreg[j][i], dS[i]);
-        }
-        lds_barrier();
-        stage_state();
     };
 
-    if constexpr (PREFETCH) {
-        ChunkRegs ra, rb;
-        if (nck > 0)
-            load_chunk(ra, 0);
-        for (int c = 0; c < nck; c += 2) {
-            step(ra, rb, c);
-            if (c + 1 < nck)
-                step(rb, ra, c + 1);
-        }
-    } else {
-        ChunkRegs r;
-        for (int c = 0; c < nck; ++c)
-            step(r, r, c);
+    for (int c = 0; c < nck; c += 2) {
+        dma_barrier();  // chunk c is in BA; every wave is done with BB
+        if (c + 1 < nck)
+            issue_chunk(BB, c + 1);
+        compute(BA, c);
+        if (c + 1 >= nck)
+            break;
+        dma_barrier();
+        if (c + 2 < nck)
+            issue_chunk(BA, c + 2);
+        compute(BB, c + 1);
     }
 
+    float *np = p.new_state + n * p.ns_sn + h * p.ns_sh + (int64_t)(v0w + lr) * p.ns_sv + 8 * lg;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int vv = v0 + 4 * lg + i, kc = 16 * (2 * w + j) + lr;
-            p.new_state[n * p.ns_sn + h * p.ns_sh + vv * p.ns_sv + kc] = Sreg[j][i];
-        }
+    for (int s = 0; s < 4; ++s) {
+        *(f32x4 *)(np + 32 * s) = S[2 * s];
+        *(f32x4 *)(np + 32 * s + 4) = S[2 * s + 1];
+    }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
-gdn_prefill_scan_kernel(ScanArgs p)
+__global__ __launch_bounds__(512) void gdn_prefill_scan8_kernel(ScanArgs p)
 {
-    scan_body<true>(p);
+    __shared__ ScanBuf<8> bufA, bufB;
+    scan_body<8>(p, bufA, bufB);
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void
-gdn_prefill_scan_kernel_nopf3(ScanArgs p)
+__global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p)
 {
-    scan_body<false>(p);
-}
-
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void
-gdn_prefill_scan_kernel_nopf4(ScanArgs p)
-{
-    scan_body<false>(p);
+    __shared__ ScanBuf<4> bufA, bufB;
+    scan_body<4>(p, bufA, bufB);
 }
 
 }  // namespace gdn
@@ -799,8 +833,17 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         if (p->q_stride[i] % 8 || p->k_stride[i] % 8 || p->output_stride[i] % 8)
             return gdn_set_error(GDN_ELAYOUT,
                                  "gdn_prefill: q/k/output strides must be multiples of 8");
-    if (!aligned(p->q, 16) || !aligned(p->k, 16) || !aligned(p->output, 16))
-        return gdn_set_error(GDN_ELAYOUT, "gdn_prefill: q/k/output must be 16-byte aligned");
+    for (int i = 0; i < 2; ++i)
+        if (p->v_stride[i] % 8)
+            return gdn_set_error(GDN_ELAYOUT, "gdn_prefill: v strides must be multiples of 8");
+    if (!aligned(p->q, 16) || !aligned(p->k, 16) || !aligned(p->v, 16) || !aligned(p->output, 16))
+        return gdn_set_error(GDN_ELAYOUT, "gdn_prefill: q/k/v/output must be 16-byte aligned");
+    for (int i = 0; i < 3; ++i)
+        if (p->new_state_stride[i] % 4 || (p->state && p->state_stride[i] % 4))
+            return gdn_set_error(GDN_ELAYOUT,
+                                 "gdn_prefill: state strides must be multiples of 4");
+    if (!aligned(p->new_state, 16) || (p->state && !aligned(p->state, 16)))
+        return gdn_set_error(GDN_ELAYOUT, "gdn_prefill: state must be 16-byte aligned");
     // the kernels address a 64-token chunk with 32-bit byte offsets
     const int64_t kMaxStride = int64_t(1) << 24;
     for (int i = 0; i < 2; ++i)
@@ -877,6 +920,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         qa.HQK = HQK;
         qa.HV = HV;
         qa.ratio = ratio;
+        qa.scale = p->scale;
         const int64_t units = L.nc * HQK;  // (chunk, q/k head) groups
         const int64_t blocks = 8 * (int64_t)ratio * ((units + 7) / 8);
         if (blocks > 0x7fffffff)
@@ -919,24 +963,22 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         sa.HQK = HQK;
         sa.HV = HV;
         sa.ratio = ratio;
-        sa.scale = p->scale;
         const int64_t ngroups = (int64_t)N * HQK;
         sa.ngroups = (int)ngroups;
-        const int64_t blocks = 8 * (8 * (int64_t)ratio) * ((ngroups + 7) / 8);
+        // 8 waves per workgroup = one (sequence, v-head) each, two waves per SIMD; with
+        // few (sequence, v-head) pairs, 4 waves and two workgroups per pair spread the
+        // state rows over twice as many CUs. variant: 1 forces 4 waves, 2 forces 8.
+        const bool nw4 = p->variant == 1 || (p->variant != 2 && (int64_t)N * HV <= 128);
+        const int tph = nw4 ? 2 : 1;
+        const int64_t blocks = 8 * ((int64_t)tph * ratio) * ((ngroups + 7) / 8);
         if (ngroups > 0x7fffffff || blocks > 0x7fffffff)
             return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
-        // variant (tuning sweeps): 0 = per-chunk batched loads at 3 waves per SIMD (the
-        // fastest on MI355X), 1 = next-chunk register prefetch at 2 waves per SIMD,
-        // 2 = batched loads at 4 waves per SIMD
-        if (p->variant == 1)
-            hipLaunchKernelGGL(gdn::gdn_prefill_scan_kernel, dim3((unsigned)blocks), dim3(256),
+        if (nw4)
+            hipLaunchKernelGGL(gdn::gdn_prefill_scan4_kernel, dim3((unsigned)blocks), dim3(256),
                                0, st, sa);
-        else if (p->variant == 2)
-            hipLaunchKernelGGL(gdn::gdn_prefill_scan_kernel_nopf4, dim3((unsigned)blocks),
-                               dim3(256), 0, st, sa);
         else
-            hipLaunchKernelGGL(gdn::gdn_prefill_scan_kernel_nopf3, dim3((unsigned)blocks),
-                               dim3(256), 0, st, sa);
+            hipLaunchKernelGGL(gdn::gdn_prefill_scan8_kernel, dim3((unsigned)blocks), dim3(512),
+                               0, st, sa);
         rc = gdn_check_launch("gdn_prefill_scan_kernel");
         if (rc)
             return rc;
