@@ -523,12 +523,12 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     constexpr int NWIN = 32 + VWIN + 19;       // all windows
     constexpr int PER = (NWIN + NW - 1) / NW;  // windows per wave
 
-    auto issue_chunk = [&](ScanBuf<NW> &B, int c) {
+    // Window i (compile-time) of this wave's share of chunk c.
+    auto issue_win = [&](ScanBuf<NW> &B, int c, const int i) {
         const int lenc = min(kC, len - c * kC);
         const char *kc_ = kbase + c * kstep, *qc_ = qbase + c * qstep, *vc_ = vbase + c * vstep;
         const char *rc_ = rbase + c * rstep;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        {
             const int win = w + NW * i;  // window kind is a compile-time function of i
             if (NW * i < 16) {
                 const int t = 4 * win + (l >> 4), cs = l & 15;
@@ -561,6 +561,11 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 }
             }
         }
+    };
+    auto issue_chunk = [&](ScanBuf<NW> &B, int c) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            issue_win(B, c, i);
     };
 
     // ---- LDS read offsets (bytes within a ScanBuf member; chunk-invariant)
@@ -596,85 +601,137 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         }
     }
 
-    auto compute = [&](ScanBuf<NW> &B, int c) {
+    // Operand reads run one step ahead of the MFMAs that consume them; sched_barrier
+    // keeps each step's reads, VALU work and MFMAs in the order written.
+    // The next chunk's copies (PER windows) are spread over phases (a) and (c): issued
+    // all at once they queue behind each other and stall the issuing waves.
+    auto compute = [&](ScanBuf<NW> &B, int c, ScanBuf<NW> &Bn, bool more) {
         const int lenc = min(kC, len - c * kC);
+        auto dma_at = [&](const int slot) {  // slots 0..7: after (a) steps 0..3, (c) tiles 0..3
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+                if ((i * 8) / PER == slot && more)
+                    issue_win(Bn, c + 1, i);
+        };
         const char *Kb = (const char *)B.K, *Qb = (const char *)B.Q, *Vb = (const char *)B.V;
         const char *Th = (const char *)B.T[0], *Tl = (const char *)B.T[1];
         const char *Pb = (const char *)B.P, *Gb = (const char *)B.G;
-
-        // (a) S0 as MFMA operands (hi + lo), X = K S0^T
-        u32x4 Bh[4], Bl[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        auto kA = [&](int s, int tt) {
+            return *(const u32x4 *)(Kb + koffA[s] + 256 * (32 * (tt >> 1) + 4 * (tt & 1)));
+        };
+        auto split_s = [&](int s, u32x4 &bh, u32x4 &bl) {
             uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
             split_bf16x2(S[2 * s][0], S[2 * s][1], h0, l0);
             split_bf16x2(S[2 * s][2], S[2 * s][3], h1, l1);
             split_bf16x2(S[2 * s + 1][0], S[2 * s + 1][1], h2, l2);
             split_bf16x2(S[2 * s + 1][2], S[2 * s + 1][3], h3, l3);
-            Bh[s] = u32x4{h0, h1, h2, h3};
-            Bl[s] = u32x4{l0, l1, l2, l3};
-        }
+            bh = u32x4{h0, h1, h2, h3};
+            bl = u32x4{l0, l1, l2, l3};
+        };
+
+        // (a) S0 as MFMA operands (hi + lo), X = K S0^T
+        u32x4 Bh[4], Bl[4], ka[2][4];
         f32x4 X[4];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+        for (int tt = 0; tt < 4; ++tt) {
+            ka[0][tt] = kA(0, tt);
             X[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        split_s(0, Bh[0], Bl[0]);
+        u32x2 vv[4];
+        f32x4 gm[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < 4; ++s) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (s < 3) {
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt)
+                    ka[(s + 1) & 1][tt] = kA(s + 1, tt);
+                split_s(s + 1, Bh[s + 1], Bl[s + 1]);
+            } else {
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) {  // (b)'s operands
+                    const int trow = 32 * (tt >> 1) + 4 * (tt & 1);
+                    vv[tt] = lds_tr16(Vb + voff + 32 * NW * trow);
+                    gm[tt] = *(const f32x4 *)(Gb + goff + 4 * trow);
+                }
+            }
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
-                const u32x4 a = *(const u32x4 *)(Kb + koffA[s] + 256 * (32 * (tt >> 1) + 4 * (tt & 1)));
-                X[tt] = mfma_bf16(a, Bh[s], X[tt]);
-                X[tt] = mfma_bf16(a, Bl[s], X[tt]);
+                X[tt] = mfma_bf16(ka[s & 1][tt], Bh[s], X[tt]);
+                X[tt] = mfma_bf16(ka[s & 1][tt], Bl[s], X[tt]);
             }
+            dma_at(s);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 
         // (b) R = V - gamma X -> operands (hi + lo) over token blocks s'
         u32x4 Rh[2], Rl[2];
+        auto tRead = [&](int tt, int sp, u32x4 &th, u32x4 &tl) {
+            const uint32_t o = toff[tt & 1] + 512 * (8 * (tt >> 1) + 2 * sp);
+            th = *(const u32x4 *)(Th + o);
+            tl = *(const u32x4 *)(Tl + o);
+        };
+        u32x4 tA[2][2][2];  // [buffer][sp][hi / lo]
+        tRead(0, 0, tA[0][0][0], tA[0][0][1]);
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
-            const int trow = 32 * (tt >> 1) + 4 * (tt & 1);
-            const u32x2 vv = lds_tr16(Vb + voff + 32 * NW * trow);
-            const f32x4 gm = *(const f32x4 *)(Gb + goff + 4 * trow);
-            const float r0 = fmaf(-gm[0], X[tt][0], bf16lo(vv[0]));
-            const float r1 = fmaf(-gm[1], X[tt][1], bf16hi(vv[0]));
-            const float r2 = fmaf(-gm[2], X[tt][2], bf16lo(vv[1]));
-            const float r3 = fmaf(-gm[3], X[tt][3], bf16hi(vv[1]));
+            const float r0 = fmaf(-gm[tt][0], X[tt][0], bf16lo(vv[tt][0]));
+            const float r1 = fmaf(-gm[tt][1], X[tt][1], bf16hi(vv[tt][0]));
+            const float r2 = fmaf(-gm[tt][2], X[tt][2], bf16lo(vv[tt][1]));
+            const float r3 = fmaf(-gm[tt][3], X[tt][3], bf16hi(vv[tt][1]));
             uint32_t h01, l01, h23, l23;
             split_bf16x2(r0, r1, h01, l01);
             split_bf16x2(r2, r3, h23, l23);
-            if (tt & 1) {
-                Rh[tt >> 1][2] = h01; Rh[tt >> 1][3] = h23;
-                Rl[tt >> 1][2] = l01; Rl[tt >> 1][3] = l23;
-            } else {
-                Rh[tt >> 1][0] = h01; Rh[tt >> 1][1] = h23;
-                Rl[tt >> 1][0] = l01; Rl[tt >> 1][1] = l23;
-            }
+            const int e = 2 * (tt & 1);
+            Rh[tt >> 1][e] = h01; Rh[tt >> 1][e + 1] = h23;
+            Rl[tt >> 1][e] = l01; Rl[tt >> 1][e + 1] = l23;
         }
 
         // (c) U = T' R
         f32x4 U[4];
+        f32x4 dc[4];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int cb = tt & 1;
+            if (tt < 3) {  // next tile's T' blocks
+#pragma unroll
+                for (int sp = 0; sp <= ((tt + 1) >> 1); ++sp)
+                    tRead(tt + 1, sp, tA[cb ^ 1][sp][0], tA[cb ^ 1][sp][1]);
+            } else {
+#pragma unroll
+                for (int t2 = 0; t2 < 4; ++t2)  // (d)'s operands
+                    dc[t2] = *(const f32x4 *)(Gb + 256 + goff + 4 * (32 * (t2 >> 1) + 4 * (t2 & 1)));
+            }
             U[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int sp = 0; sp <= (tt >> 1); ++sp) {
-                const uint32_t o = toff[tt & 1] + 512 * (8 * (tt >> 1) + 2 * sp);
-                const u32x4 th = *(const u32x4 *)(Th + o);
-                const u32x4 tl = *(const u32x4 *)(Tl + o);
-                U[tt] = mfma_bf16(th, Rh[sp], U[tt]);
-                U[tt] = mfma_bf16(th, Rl[sp], U[tt]);
-                U[tt] = mfma_bf16(tl, Rh[sp], U[tt]);
+                U[tt] = mfma_bf16(tA[cb][sp][0], Rh[sp], U[tt]);
+                U[tt] = mfma_bf16(tA[cb][sp][0], Rl[sp], U[tt]);
+                U[tt] = mfma_bf16(tA[cb][sp][1], Rh[sp], U[tt]);
             }
+            dma_at(4 + tt);
         }
+        __builtin_amdgcn_sched_barrier(0);
 
         // (d) W = dec U (hi + lo) for the state update, U (bf16) for the readout
+        auto qRead = [&](int tt, u32x4 *qv, u32x4 *pv) {
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+                qv[s2] = *(const u32x4 *)(Qb + qoff[s2] + 4096 * tt);
+#pragma unroll
+            for (int sp = 0; sp <= (tt >> 1); ++sp)
+                pv[sp] = *(const u32x4 *)(Pb + poff[tt & 1] + 512 * (4 * tt + 2 * sp));
+        };
+        u32x4 qA[2][4], pA[2][2];
+        qRead(0, qA[0], pA[0]);
         u32x4 Wh[2], Wl[2], Ub[2];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
-            const int trow = 32 * (tt >> 1) + 4 * (tt & 1);
-            const f32x4 dc = *(const f32x4 *)(Gb + 256 + goff + 4 * trow);
             uint32_t h01, l01, h23, l23;
-            split_bf16x2(dc[0] * U[tt][0], dc[1] * U[tt][1], h01, l01);
-            split_bf16x2(dc[2] * U[tt][2], dc[3] * U[tt][3], h23, l23);
+            split_bf16x2(dc[tt][0] * U[tt][0], dc[tt][1] * U[tt][1], h01, l01);
+            split_bf16x2(dc[tt][2] * U[tt][2], dc[tt][3] * U[tt][3], h23, l23);
             const uint32_t u01 = pack_bf16x2(U[tt][0], U[tt][1]), u23 = pack_bf16x2(U[tt][2], U[tt][3]);
             const int e = 2 * (tt & 1);
             Wh[tt >> 1][e] = h01; Wh[tt >> 1][e + 1] = h23;
@@ -682,55 +739,67 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
             Ub[tt >> 1][e] = u01; Ub[tt >> 1][e + 1] = u23;
         }
 
-        // (e) O^T = scale gamma S0 Q^T + U^T P'^T; lane (t = 16 tt + lr) stores 4 values
-        char *oc_ = obase + c * ostep;
+        // (e) O^T = scale gamma S0 Q^T + U^T P'^T; lane (t = 16 tt + lr) stores 4 values.
+        // Rows past the chunk's end fall outside the buffer range and are dropped.
+        const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+            obase + c * ostep, 0, (int)((uint32_t)lenc * ost2), 0x00020000);
+        auto ktRead = [&](int gidx, u32x4 *ko) {
+            const int s2 = gidx >> 1, hh = gidx & 1;
+#pragma unroll
+            for (int sp = 0; sp < 2; ++sp) {
+                const u32x2 k0 = lds_tr16(Kb + ktoff[s2] + 256 * (32 * sp) + 8 * hh);
+                const u32x2 k1 = lds_tr16(Kb + ktoff[s2] + 256 * (32 * sp + 4) + 8 * hh);
+                ko[sp] = u32x4{k0[0], k0[1], k1[0], k1[1]};
+            }
+        };
+        u32x4 kt[2][2];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int cb = tt & 1;
+            if (tt < 3)
+                qRead(tt + 1, qA[cb ^ 1], pA[cb ^ 1]);
+            else
+                ktRead(0, kt[0]);  // (f)'s first operands
             f32x4 Oi = {0.f, 0.f, 0.f, 0.f}, Oa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                Oi = mfma_bf16(Bh[s], *(const u32x4 *)(Qb + qoff[s] + 4096 * tt), Oi);
+            for (int s2 = 0; s2 < 4; ++s2)
+                Oi = mfma_bf16(Bh[s2], qA[cb][s2], Oi);
 #pragma unroll
             for (int sp = 0; sp <= (tt >> 1); ++sp)
-                Oa = mfma_bf16(Ub[sp], *(const u32x4 *)(Pb + poff[tt & 1] + 512 * (4 * tt + 2 * sp)), Oa);
+                Oa = mfma_bf16(Ub[sp], pA[cb][sp], Oa);
             const float sg = *(const float *)(Gb + 512 + sgoff + 64 * tt);
             const uint32_t o01 = pack_bf16x2(fmaf(sg, Oi[0], Oa[0]), fmaf(sg, Oi[1], Oa[1]));
             const uint32_t o23 = pack_bf16x2(fmaf(sg, Oi[2], Oa[2]), fmaf(sg, Oi[3], Oa[3]));
-            const int t = 16 * tt + lr;
-            if (t < lenc)
-                *(u32x2 *)(oc_ + (uint32_t)t * ost2 + 8u * lg) = u32x2{o01, o23};
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{o01, o23}, orsrc,
+                                                  (int)((uint32_t)(16 * tt + lr) * ost2 + 8u * lg), 0, 0);
         }
 
         // (f) S = gammaC S0 + W^T K
         const float gC = *(const float *)(Gb + 768);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int gidx = 0; gidx < 8; ++gidx) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (gidx < 7)
+                ktRead(gidx + 1, kt[(gidx + 1) & 1]);
+            f32x4 acc = gC * S[gidx];
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                f32x4 acc = gC * S[2 * s + hh];
-#pragma unroll
-                for (int sp = 0; sp < 2; ++sp) {
-                    const u32x2 k0 = lds_tr16(Kb + ktoff[s] + 256 * (32 * sp) + 8 * hh);
-                    const u32x2 k1 = lds_tr16(Kb + ktoff[s] + 256 * (32 * sp + 4) + 8 * hh);
-                    const u32x4 a = {k0[0], k0[1], k1[0], k1[1]};
-                    acc = mfma_bf16(a, Wh[sp], acc);
-                    acc = mfma_bf16(a, Wl[sp], acc);
-                }
-                S[2 * s + hh] = acc;
+            for (int sp = 0; sp < 2; ++sp) {
+                acc = mfma_bf16(kt[gidx & 1][sp], Wh[sp], acc);
+                acc = mfma_bf16(kt[gidx & 1][sp], Wl[sp], acc);
             }
+            S[gidx] = acc;
+        }
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     for (int c = 0; c < nck; c += 2) {
         dma_barrier();  // chunk c is in BA; every wave is done with BB
-        if (c + 1 < nck)
-            issue_chunk(BB, c + 1);
-        compute(BA, c);
+        compute(BA, c, BB, c + 1 < nck);
         if (c + 1 >= nck)
             break;
         dma_barrier();
-        if (c + 2 < nck)
-            issue_chunk(BA, c + 2);
-        compute(BB, c + 1);
+        compute(BB, c + 1, BA, c + 2 < nck);
     }
 
     float *np = p.new_state + n * p.ns_sn + h * p.ns_sh + (int64_t)(v0w + lr) * p.ns_sv + 8 * lg;
