@@ -181,247 +181,6 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
     }
 }
 
-// ------------------------------------------------------------------------- prep
-struct PrepArgs {
-    const bf16_t *q, *k, *a, *b;
-    const float *A_log, *dt_bias;
-    int64_t q_st, q_sh, k_st, k_sh, a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
-    const int32_t *header, *chunk_tok0, *chunk_len;
-    char *records;
-    int HQK, HV, ratio;
-    float scale;
-};
-
-// Lower-triangular 16x16 tile t of a 64x64 matrix -> (row block, column block).
-__device__ __forceinline__ int tile_i(int t) { return t < 1 ? 0 : (t < 3 ? 1 : (t < 6 ? 2 : 3)); }
-__device__ __forceinline__ int tile_j(int t) { return t - tri_blk(tile_i(t), 0); }
-
-__device__ __forceinline__ float quad_bcast_sel(float x, int k)
-{
-    switch (k & 3) {
-    case 0: return quad_bcast<0>(x);
-    case 1: return quad_bcast<1>(x);
-    case 2: return quad_bcast<2>(x);
-    default: return quad_bcast<3>(x);
-    }
-}
-
-__global__ __launch_bounds__(256) void gdn_prefill_prep_kernel(PrepArgs p)
-{
-    // One workgroup per (chunk, v-head). The `ratio` v-heads of one (chunk, q/k head)
-    // read the same K and Q: their workgroups land on one XCD (ids are dealt to the 8
-    // XCDs round-robin), so the second read hits that XCD's L2.
-    const int pid = blockIdx.x, xcd = pid & 7, slot = pid >> 3;
-    const int hh = slot % p.ratio;
-    const int grp = (slot / p.ratio) * 8 + xcd;
-    const int c = grp / p.HQK, g = grp % p.HQK;
-    if (c >= p.header[0])
-        return;
-    const int h = g * p.ratio + hh;
-    const int tok0 = p.chunk_tok0[c];
-    const int len = p.chunk_len[c];
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
-
-    // K and Q (bf16) first; the same bytes then hold A and T (fp32).
-    __shared__ __align__(16) char smem[2 * kC * kLdK * 2];
-    __shared__ __align__(16) bf16_t Ps[10 * kBlk];
-    __shared__ __align__(16) float Ms[4][16][17];
-    __shared__ float Lg[kC], Bt[kC];
-    bf16_t(*Ks)[kLdK] = (bf16_t(*)[kLdK])smem;
-    bf16_t(*Qs)[kLdK] = (bf16_t(*)[kLdK])(smem + kC * kLdK * 2);
-    float(*As)[kC + 4] = (float(*)[kC + 4])smem;
-    float(*Ts)[kC + 4] = (float(*)[kC + 4])(smem + kC * (kC + 4) * 4);
-    static_assert(2 * kC * (kC + 4) * 4 == 2 * kC * kLdK * 2, "A/T alias K/Q exactly");
-
-    char *rec = p.records + ((int64_t)c * p.HV + h) * kRecBytes;
-
-    // Wave 0's gate inputs (one token per lane) are requested first, then K and Q.
-    uint32_t a_raw = 0u, b_raw = 0u;
-    if (w == 0) {
-        const int t = tok0 + min(l, len - 1);
-        a_raw = p.a[(int64_t)t * p.a_st + h * p.a_sh];
-        b_raw = p.b[(int64_t)t * p.b_st + h * p.b_sh];
-    }
-    // K, Q chunk rows -> LDS. All eight 16-byte loads per lane are issued before the
-    // first store. Rows past the chunk's end repeat its last token: they only meet
-    // beta = 0 (in A) or the causal mask (in P), so they contribute nothing.
-    {
-        u32x4 kv[4], qv[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int s = tid + 256 * m, row = min(s >> 4, len - 1), col = (s & 15) * 8;
-            kv[m] = *(const u32x4 *)(p.k + (int64_t)(tok0 + row) * p.k_st + g * p.k_sh + col);
-            qv[m] = *(const u32x4 *)(p.q + (int64_t)(tok0 + row) * p.q_st + g * p.q_sh + col);
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int s = tid + 256 * m, row = s >> 4, col = (s & 15) * 8;
-            *(u32x4 *)&Ks[row][col] = kv[m];
-            *(u32x4 *)&Qs[row][col] = qv[m];
-        }
-    }
-
-    // Gates and in-chunk cumulative log decay: wave 0, one lane per token
-    // (gdn_decode/solution/triton/kernel.py:128-131). Padding tokens: alpha = 1, beta = 0.
-    if (w == 0) {
-        float la = 0.f, bt = 0.f;
-        if (l < len) {
-            const float x = bf16_to_f32(a_raw) + p.dt_bias[h * p.dt_s];
-            const float sp = x > 20.f ? x : logf(1.f + expf(x));
-            la = -expf(p.A_log[h * p.A_log_s]) * sp;
-            bt = 1.f / (1.f + expf(-bf16_to_f32(b_raw)));
-        }
-        // cumulative decay in log2 units: every decay factor below is 2^(non-positive
-        // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow)
-        float L = la * 1.44269504088896340736f;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(L, off, 64);
-            if (l >= off)
-                L += y;
-        }
-        const float Lend = __shfl(L, 63, 64);
-        Lg[l] = L;
-        Bt[l] = bt;
-        float *gates = (float *)(rec + kRecGates);
-        const float gam = __builtin_amdgcn_exp2f(L);
-        gates[l] = gam;
-        gates[64 + l] = __builtin_amdgcn_exp2f(Lend - L);
-        gates[128 + l] = p.scale * gam;
-        if (l == 0)
-            gates[192] = __builtin_amdgcn_exp2f(Lend);
-        if (l < 4)
-            ((float *)(rec + kRecZero))[l] = 0.f;
-    }
-    lds_barrier();
-
-    // 20 tile jobs (10 lower tiles of K K^T, 10 of Q K^T), 5 per wave.
-    f32x4 acc[5];
-#pragma unroll
-    for (int m = 0; m < 5; ++m) {
-        const int job = w + 4 * m;
-        const bool isq = job >= 10;
-        const int t = isq ? job - 10 : job;
-        const int ti = tile_i(t), tj = tile_j(t);
-        f32x4 r = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const u32x4 a = isq ? *(const u32x4 *)&Qs[16 * ti + lr][ks * 32 + 8 * lg]
-                                : *(const u32x4 *)&Ks[16 * ti + lr][ks * 32 + 8 * lg];
-            const u32x4 bk = *(const u32x4 *)&Ks[16 * tj + lr][ks * 32 + 8 * lg];
-            r = mfma_bf16(a, bk, r);
-        }
-        acc[m] = r;
-        if (isq) {  // P' = scale exp(L_t - L_j) q_t . k_j for j <= t, bf16, block layout
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int tt = 16 * ti + 4 * lg + e, jj = 16 * tj + lr;
-                const float pv =
-                    jj <= tt ? p.scale * __builtin_amdgcn_exp2f(Lg[tt] - Lg[jj]) * r[e] : 0.f;
-                Ps[t * kBlk + (4 * lg + e) * 16 + lr] = (bf16_t)f32_to_bf16(pv);
-            }
-        }
-    }
-    lds_barrier();  // K and Q are no longer read: their bytes become A and T
-
-    // A[t,j] = beta_t exp(L_t - L_j) k_t . k_j, j < t
-#pragma unroll
-    for (int m = 0; m < 5; ++m) {
-        const int job = w + 4 * m;
-        if (job < 10) {
-            const int ti = tile_i(job), tj = tile_j(job);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int tt = 16 * ti + 4 * lg + e, jj = 16 * tj + lr;
-                As[tt][jj] = jj < tt ? Bt[tt] * __builtin_amdgcn_exp2f(Lg[tt] - Lg[jj]) * acc[m][e] : 0.f;
-            }
-        }
-    }
-    for (int q = tid; q < 10 * kBlk / 8; q += 256)
-        *(u32x4 *)(rec + kRecP + q * 16) = *(const u32x4 *)((const char *)Ps + q * 16);
-    lds_barrier();
-
-    // Diagonal blocks of T = (I + A)^-1: wave i inverts block i by right-looking
-    // substitution; lane = 4 * column + row group, each lane holding rows g4 + 4m.
-    {
-        const int o = 16 * w, col = l >> 2, g4 = l & 3;
-        float x[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-            x[m] = (g4 + 4 * m == col) ? 1.f : 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float xr = quad_bcast_sel(x[r >> 2], r & 3);  // final x_r of this column
-#pragma unroll
-            for (int m = 0; m < 4; ++m)  // A is zero on and above the diagonal
-                x[m] = fmaf(-As[o + g4 + 4 * m][o + r], xr, x[m]);
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-            Ts[o + g4 + 4 * m][o + col] = x[m];
-    }
-    lds_barrier();
-
-    // Off-diagonal blocks, one block diagonal at a time (fp32 MFMA 16x16x4):
-    //   T_ij = -T_ii * sum_{m=j}^{i-1} A_im T_mj
-    for (int d = 1; d < 4; ++d) {
-        const int i = w + d, j = w;
-        const bool active = i < 4;
-        if (active) {
-            f32x4 M = {0.f, 0.f, 0.f, 0.f};
-            for (int m = j; m < i; ++m) {
-#pragma unroll
-                for (int k4 = 0; k4 < 4; ++k4)
-                    M = mfma_f32(As[16 * i + lr][16 * m + 4 * k4 + lg],
-                                 Ts[16 * m + 4 * k4 + lg][16 * j + lr], M);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                Ms[w][4 * lg + e][lr] = M[e];
-        }
-        lds_barrier();
-        if (active) {
-            f32x4 R = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int k4 = 0; k4 < 4; ++k4)
-                R = mfma_f32(Ts[16 * i + lr][16 * i + 4 * k4 + lg], Ms[w][4 * k4 + lg][lr], R);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                Ts[16 * i + 4 * lg + e][16 * j + lr] = -R[e];
-        }
-        lds_barrier();
-    }
-
-    // T' = T diag(beta) -> record (bf16 hi / lo, block layout); 16-byte pieces. Padding
-    // tokens have beta = 0, so their columns of T' are zero.
-    for (int q = tid; q < 10 * kBlk / 8; q += 256) {
-        const int bidx = q >> 5, row = (q & 31) >> 1, c8 = (q & 1) * 8;
-        const int bi = tile_i(bidx), bj = tile_j(bidx);
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int j0 = 16 * bj + c8 + 2 * e;
-            split_bf16x2(Ts[16 * bi + row][j0] * Bt[j0], Ts[16 * bi + row][j0 + 1] * Bt[j0 + 1],
-                         hw[e], lw[e]);
-        }
-        *(u32x4 *)(rec + kRecThi + q * 16) = u32x4{hw[0], hw[1], hw[2], hw[3]};
-        *(u32x4 *)(rec + kRecTlo + q * 16) = u32x4{lw[0], lw[1], lw[2], lw[3]};
-    }
-}
-
-// ------------------------------------------------------------------------- scan
-struct ScanArgs {
-    const bf16_t *q, *k, *v;
-    const float *state;
-    float *new_state;
-    bf16_t *out;
-    int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
-    int64_t st_sn, st_sh, st_sv, ns_sn, ns_sh, ns_sv;
-    const int32_t *header, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
-    const char *records;
-    int HQK, HV, ratio, ngroups;
-};
-
 #define GDN_LDS __attribute__((address_space(3)))
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
@@ -446,6 +205,288 @@ __device__ __forceinline__ void dma_barrier()
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     lds_barrier();
 }
+
+// ------------------------------------------------------------------------- prep
+struct PrepArgs {
+    const bf16_t *q, *k, *a, *b;
+    const float *A_log, *dt_bias;
+    int64_t q_st, q_sh, k_st, k_sh, a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
+    const int32_t *header, *chunk_tok0, *chunk_len;
+    char *records;
+    int HQK, HV, ratio;
+    float scale;
+};
+
+// Row order inside a 16-row block used for fp32 MFMA operands: pi(m) = 4 (m % 4) + m / 4
+// (a 4 x 4 transpose, its own inverse). With pi-ordered rows an MFMA result in C layout
+// (lane (n, g) holds rows 4 g + i) already holds rows 4 i + g: exactly the operand
+// layout of the next v_mfma_f32_16x16x4_f32 (k-slice i, lane (n, g) supplies k = 4 i + g).
+__device__ __forceinline__ int pi16(int m) { return 4 * (m & 3) + (m >> 2); }
+
+// Broadcast lane K of every 16-lane row (DPP row_newbcast).
+template <int K>
+__device__ __forceinline__ float row_bcast(float x)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x150 + K, 0xF, 0xF, false));
+}
+
+// One workgroup per (chunk, q/k head, group of VH v-heads): 4 VH waves, wave (hv, w) =
+// v-head hv of the group, block w. The chunk's K and Q go to LDS once (direct copies)
+// and serve every v-head of the group. Wave (hv, w):
+//   * computes the gates and the cumulative log2 decay L of the chunk (lane = token);
+//   * writes P' row block w: P'[t, j] = scale 2^(L_t - L_j) q_t . k_j, j <= t;
+//   * forms the A blocks it needs, A[t, j] = beta_t 2^(L_t - L_j) k_t . k_j (j < t):
+//     (w, w) and (i, m) for w <= m < i;
+//   * inverts X_w = (I + A_ww)^-1 by forward substitution (DPP broadcasts);
+//   * after a barrier (all X_i published): column block w of T = (I + A)^-1,
+//       T_ww = X_w,  T_iw = -X_i sum_{m=w}^{i-1} A_im T_mw  (i > w),
+//     on fp32 MFMA with every operand in registers, and writes T' = T diag(beta).
+// (gdn_prefill/solution/triton/kernel.py:60-79 form the same A, T and P.)
+template <int VH>
+__device__ __forceinline__ void prep_body(const PrepArgs &p)
+{
+    const int ngrp = p.ratio / VH;
+    const int pid = blockIdx.x, xcd = pid & 7, slot = pid >> 3;
+    const int hg = slot % ngrp;
+    const int grp = (slot / ngrp) * 8 + xcd;  // (chunk, q/k head); one XCD for all its v-heads
+    const int c = grp / p.HQK, g = grp % p.HQK;
+    if (c >= p.header[0])
+        return;
+    const int tok0 = p.chunk_tok0[c];
+    const int len = p.chunk_len[c];
+    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
+    // Waves are dealt to the 4 SIMDs round-robin: the second v-head takes the blocks in
+    // reverse, so each SIMD pairs a heavy column block (w = 0) with a light one.
+    const int hv = wv >> 2, w = hv & 1 ? 3 - (wv & 3) : (wv & 3);
+    const int h = g * p.ratio + hg * VH + hv;
+    char *rec = p.records + ((int64_t)c * p.HV + h) * kRecBytes;
+
+    __shared__ u32x4 Ks[kC * 16], Qs[kC * 16];  // row t, k-chunk c at unit 16 t + (c ^ (t & 15))
+    __shared__ float Ls[VH][64];           // L by token
+    __shared__ float LsT[VH][64];          // L of token 16 b + 4 i + g at 16 b + 4 g + i
+    __shared__ float Bs[VH][64];           // beta by token
+    __shared__ __align__(16) float Ms[4 * VH][16][16];     // per wave: A_ww rows, then X_w
+    __shared__ f32x4 XA[VH][4][64];        // X_w in A-operand layout, by lane
+    __shared__ __align__(16) uint16_t Tst[4 * VH][2][256];  // per wave: one T' block, hi / lo
+
+    // K, Q -> LDS: 32 windows of 64 16-byte units (4 rows each), dealt to the waves.
+    // Rows past the chunk's end repeat its last token: they meet beta = 0 or the causal
+    // mask only.
+    {
+        const char *kb = (const char *)(p.k + (int64_t)tok0 * p.k_st + g * p.k_sh);
+        const char *qb = (const char *)(p.q + (int64_t)tok0 * p.q_st + g * p.q_sh);
+        const uint32_t kst2 = (uint32_t)p.k_st * 2, qst2 = (uint32_t)p.q_st * 2;
+#pragma unroll
+        for (int i = 0; i < 8 / VH; ++i) {
+            const int win = wv + 4 * VH * i;
+            const int isq = win >= 16, b = win & 15;
+            const int t = 4 * b + (l >> 4), cs = l & 15;
+            const uint32_t off = (uint32_t)min(t, len - 1) * (isq ? qst2 : kst2) + 16u * (cs ^ (t & 15));
+            dma16((isq ? qb : kb) + off, isq ? &Qs[64 * b] : &Ks[64 * b]);
+        }
+    }
+
+    // Gates (gdn_decode/solution/triton/kernel.py:128-131); padding tokens: alpha = 1,
+    // beta = 0. Cumulative decay in log2 units: every factor below is 2^(non-positive
+    // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow).
+    if (w == 0) {
+        const int tl = tok0 + min(l, len - 1);
+        const float a_in = bf16_to_f32(p.a[(int64_t)tl * p.a_st + h * p.a_sh]);
+        const float b_in = bf16_to_f32(p.b[(int64_t)tl * p.b_st + h * p.b_sh]);
+        float la = 0.f, bt = 0.f;
+        if (l < len) {
+            const float x = a_in + p.dt_bias[h * p.dt_s];
+            const float sp = x > 20.f ? x : logf(1.f + expf(x));
+            la = -expf(p.A_log[h * p.A_log_s]) * sp;
+            bt = 1.f / (1.f + expf(-b_in));
+        }
+        float L = la * 1.44269504088896340736f;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(L, off, 64);
+            if (l >= off)
+                L += y;
+        }
+        const float Lend = __shfl(L, 63, 64);
+        Ls[hv][l] = L;
+        Bs[hv][l] = bt;
+        LsT[hv][16 * (l >> 4) + 4 * (l & 3) + ((l >> 2) & 3)] = L;
+        float *gates = (float *)(rec + kRecGates);
+        const float gam = __builtin_amdgcn_exp2f(L);
+        gates[l] = gam;
+        gates[64 + l] = __builtin_amdgcn_exp2f(Lend - L);
+        gates[128 + l] = p.scale * gam;
+        if (l == 0)
+            gates[192] = __builtin_amdgcn_exp2f(Lend);
+        if (l < 4)
+            ((float *)(rec + kRecZero))[l] = 0.f;
+    }
+    dma_barrier();  // K, Q, L, beta visible to every wave
+
+    // MFMA operand: 16 rows (row(lr) of block b), k-chunk 4 ks + lg.
+    auto kop = [&](const u32x4 *M, int row, int ks) {
+        return M[16 * row + ((4 * ks + lg) ^ (row & 15))];
+    };
+
+    // P' row block w: lane (t = 16 w + lr, lg) holds columns 16 jb + 4 lg .. +3.
+    {
+        const int t = 16 * w + lr;
+        const float Lt = Ls[hv][t];
+        u32x4 qn[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            qn[ks] = kop(Qs, t, ks);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            if (jb > w)
+                break;
+            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                r = mfma_bf16(kop(Ks, 16 * jb + lr, ks), qn[ks], r);
+            const f32x4 Lj = *(const f32x4 *)&Ls[hv][16 * jb + 4 * lg];
+            float pv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 16 * jb + 4 * lg + e;
+                pv[e] = j <= t ? p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * r[e] : 0.f;
+            }
+            *(u32x2 *)(rec + kRecP + 2 * (tri_blk(w, jb) * kBlk + lr * 16 + 4 * lg)) =
+                u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+        }
+    }
+
+    // A blocks (i, m): lane (lr, lg) element e = A[16 i + pi(lr)][16 m + 4 e + lg].
+    f32x4 Ar[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int m = 0; m <= i; ++m) {
+            Ar[i][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (i == m ? m != w : m < w)
+                continue;
+            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                r = mfma_bf16(kop(Ks, 16 * m + pi16(lr), ks), kop(Ks, 16 * i + pi16(lr), ks), r);
+            const int t = 16 * i + pi16(lr);
+            const float Lt = Ls[hv][t], btt = Bs[hv][t];
+            const f32x4 Lm = *(const f32x4 *)&LsT[hv][16 * m + 4 * lg];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 16 * m + 4 * e + lg;
+                Ar[i][m][e] = j < t ? btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * r[e] : 0.f;
+            }
+        }
+
+    // X_w = (I + A_ww)^-1. Lane (lr, lg) holds row pi(lr), columns lg + 4 s (s = 0..3)
+    // of X; step m subtracts A[r][m] x (row m of X), row m being final (A is strictly
+    // lower, so rows r <= m see A[r][m] = 0). Row m sits in lane pi(m) of every 16-lane
+    // row, next to the same columns.
+    f32x4 xw;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (i != w)
+            continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            Ms[wv][pi16(lr)][4 * e + lg] = Ar[i][i][e];
+    }
+    {
+        float arow[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 v = *(const f32x4 *)&Ms[wv][pi16(lr)][4 * q];
+            arow[4 * q] = v[0]; arow[4 * q + 1] = v[1]; arow[4 * q + 2] = v[2]; arow[4 * q + 3] = v[3];
+        }
+        float x[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            x[s2] = pi16(lr) == lg + 4 * s2 ? 1.f : 0.f;
+#define GDN_SUBST_STEP(M)                                                         \
+        {                                                                         \
+            _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2)                      \
+                x[s2] = fmaf(-arow[M], row_bcast<4 * ((M) & 3) + ((M) >> 2)>(x[s2]), x[s2]); \
+        }
+        GDN_SUBST_STEP(0) GDN_SUBST_STEP(1) GDN_SUBST_STEP(2) GDN_SUBST_STEP(3)
+        GDN_SUBST_STEP(4) GDN_SUBST_STEP(5) GDN_SUBST_STEP(6) GDN_SUBST_STEP(7)
+        GDN_SUBST_STEP(8) GDN_SUBST_STEP(9) GDN_SUBST_STEP(10) GDN_SUBST_STEP(11)
+        GDN_SUBST_STEP(12) GDN_SUBST_STEP(13) GDN_SUBST_STEP(14)
+#undef GDN_SUBST_STEP
+        xw = f32x4{x[0], x[1], x[2], x[3]};
+    }
+    XA[hv][w][l] = xw;
+    // X_w in B-operand layout (lane (n, lg) element s = X[4 s + lg][n]) via this wave's scratch
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+        Ms[wv][pi16(lr)][lg + 4 * s2] = xw[s2];
+    f32x4 TB[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+        TB[0][s2] = Ms[wv][4 * s2 + lg][lr];
+    lds_barrier();  // every X_i is in XA
+
+    // Column block w of T; TB[i] = T_(w+i),w in B-operand layout.
+#pragma unroll
+    for (int i = 1; i < 4; ++i) {
+        if (i + w > 3)
+            break;
+        f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < i; ++m) {  // block m + w
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm)
+                    if (ii == i + w && mm == m + w)
+#pragma unroll
+                        for (int s2 = 0; s2 < 4; ++s2)
+                            z = mfma_f32(Ar[ii][mm][s2], TB[m][s2], z);
+        }
+        const f32x4 xa = XA[hv][i + w][l];
+        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            t = mfma_f32(xa[s2], z[s2], t);
+        TB[i] = -t;
+    }
+
+    // T' = T diag(beta) -> record (bf16 hi / lo, block layout), one block at a time
+    // through this wave's staging area (B layout -> row-major 16-byte units).
+    const float bcol = Bs[hv][16 * w + lr];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (i + w > 3)
+            break;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const float v = TB[i][s2] * bcol;
+            const uint32_t hi = f32_to_bf16(v);
+            const uint32_t lo = f32_to_bf16(v - bf16_to_f32(hi));
+            Tst[wv][0][(4 * s2 + lg) * 16 + lr] = (uint16_t)hi;
+            Tst[wv][1][(4 * s2 + lg) * 16 + lr] = (uint16_t)lo;
+        }
+        const int half = l >> 5, u = l & 31;
+        const u32x4 unit = *(const u32x4 *)&Tst[wv][half][8 * u];
+        *(u32x4 *)(rec + (half ? kRecTlo : kRecThi) + tri_blk(i + w, w) * 512 + 16 * u) = unit;
+    }
+}
+
+__global__ __launch_bounds__(256) void gdn_prefill_prep1_kernel(PrepArgs p) { prep_body<1>(p); }
+__global__ __launch_bounds__(512) void gdn_prefill_prep2_kernel(PrepArgs p) { prep_body<2>(p); }
+
+// ------------------------------------------------------------------------- scan
+struct ScanArgs {
+    const bf16_t *q, *k, *v;
+    const float *state;
+    float *new_state;
+    bf16_t *out;
+    int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
+    int64_t st_sn, st_sh, st_sv, ns_sn, ns_sh, ns_sv;
+    const int32_t *header, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
+    const char *records;
+    int HQK, HV, ratio, ngroups;
+};
 
 // Bank swizzles (16-byte units; every operand read below covers 16 distinct bank groups):
 //   K row t, k-chunk c (k = 8c .. 8c+7)   -> unit 16 t + (c ^ kswz(t))
@@ -990,12 +1031,18 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         qa.HV = HV;
         qa.ratio = ratio;
         qa.scale = p->scale;
+        // one workgroup per (chunk, q/k head, pair of v-heads) when the ratio is even
+        const int vh = ratio % 2 == 0 ? 2 : 1;
         const int64_t units = L.nc * HQK;  // (chunk, q/k head) groups
-        const int64_t blocks = 8 * (int64_t)ratio * ((units + 7) / 8);
+        const int64_t blocks = 8 * (int64_t)(ratio / vh) * ((units + 7) / 8);
         if (blocks > 0x7fffffff)
             return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
-        hipLaunchKernelGGL(gdn::gdn_prefill_prep_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                           st, qa);
+        if (vh == 2)
+            hipLaunchKernelGGL(gdn::gdn_prefill_prep2_kernel, dim3((unsigned)blocks), dim3(512), 0,
+                               st, qa);
+        else
+            hipLaunchKernelGGL(gdn::gdn_prefill_prep1_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                               st, qa);
         rc = gdn_check_launch("gdn_prefill_prep_kernel");
         if (rc)
             return rc;
