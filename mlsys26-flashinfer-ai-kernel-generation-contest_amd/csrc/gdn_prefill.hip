@@ -25,6 +25,8 @@
 //         into bf16 hi + lo halves so the state keeps ~2^-16 relative accuracy.
 #include "gdn_common.h"
 
+#include <algorithm>
+
 namespace gdn {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -230,74 +232,83 @@ __device__ __forceinline__ float row_bcast(float x)
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x150 + K, 0xF, 0xF, false));
 }
 
-// One workgroup per (chunk, q/k head, group of VH v-heads): 4 VH waves, wave (hv, w) =
-// v-head hv of the group, block w. The chunk's K and Q go to LDS once (direct copies)
-// and serve every v-head of the group. Wave (hv, w):
-//   * computes the gates and the cumulative log2 decay L of the chunk (lane = token);
+// Work unit: (chunk, q/k head, group of VH v-heads). A persistent workgroup of 4 VH waves
+// walks units u = blockIdx.x, + gridDim.x, ...; wave (hv, w) = v-head hv of the group,
+// block w. The unit's K and Q go to LDS once (direct copies; K double-buffered, the next
+// unit's copies and gate inputs in flight while this one computes) and serve every
+// v-head of the group. Per unit, wave (hv, w):
 //   * writes P' row block w: P'[t, j] = scale 2^(L_t - L_j) q_t . k_j, j <= t;
 //   * forms the A blocks it needs, A[t, j] = beta_t 2^(L_t - L_j) k_t . k_j (j < t):
 //     (w, w) and (i, m) for w <= m < i;
 //   * inverts X_w = (I + A_ww)^-1 by forward substitution (DPP broadcasts);
 //   * after a barrier (all X_i published): column block w of T = (I + A)^-1,
 //       T_ww = X_w,  T_iw = -X_i sum_{m=w}^{i-1} A_im T_mw  (i > w),
-//     on fp32 MFMA with every operand in registers, and writes T' = T diag(beta).
+//     on fp32 MFMA with every operand in registers, and writes T' = T diag(beta);
+// wave (hv, 0) also computes the next unit's gates and cumulative log2 decay L.
 // (gdn_prefill/solution/triton/kernel.py:60-79 form the same A, T and P.)
 template <int VH>
-__device__ __forceinline__ void prep_body(const PrepArgs &p)
+struct PrepSmem {
+    u32x4 K[2][kC * 16];  // row t, k-chunk c at unit 16 t + (c ^ (t & 15))
+    u32x4 Q[kC * 16];
+    float L[2][VH][64];   // L by token
+    float LT[2][VH][64];  // L of token 16 b + 4 i + g at 16 b + 4 g + i
+    float B[2][VH][64];   // beta by token
+    f32x4 XA[VH][4][64];  // X_w in A-operand layout, by lane
+    float Ms[4 * VH][16][16];  // per wave: A_ww rows, X_w, then T' staging (bf16)
+};
+
+template <int VH>
+__device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 {
     const int ngrp = p.ratio / VH;
-    const int pid = blockIdx.x, xcd = pid & 7, slot = pid >> 3;
-    const int hg = slot % ngrp;
-    const int grp = (slot / ngrp) * 8 + xcd;  // (chunk, q/k head); one XCD for all its v-heads
-    const int c = grp / p.HQK, g = grp % p.HQK;
-    if (c >= p.header[0])
-        return;
-    const int tok0 = p.chunk_tok0[c];
-    const int len = p.chunk_len[c];
+    const int nunits = p.header[0] * p.HQK * ngrp;
     const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
     // Waves are dealt to the 4 SIMDs round-robin: the second v-head takes the blocks in
     // reverse, so each SIMD pairs a heavy column block (w = 0) with a light one.
     const int hv = wv >> 2, w = hv & 1 ? 3 - (wv & 3) : (wv & 3);
-    const int h = g * p.ratio + hg * VH + hv;
-    char *rec = p.records + ((int64_t)c * p.HV + h) * kRecBytes;
+    const uint32_t kst2 = (uint32_t)p.k_st * 2, qst2 = (uint32_t)p.q_st * 2;
 
-    __shared__ u32x4 Ks[kC * 16], Qs[kC * 16];  // row t, k-chunk c at unit 16 t + (c ^ (t & 15))
-    __shared__ float Ls[VH][64];           // L by token
-    __shared__ float LsT[VH][64];          // L of token 16 b + 4 i + g at 16 b + 4 g + i
-    __shared__ float Bs[VH][64];           // beta by token
-    __shared__ __align__(16) float Ms[4 * VH][16][16];     // per wave: A_ww rows, then X_w
-    __shared__ f32x4 XA[VH][4][64];        // X_w in A-operand layout, by lane
-    __shared__ __align__(16) uint16_t Tst[4 * VH][2][256];  // per wave: one T' block, hi / lo
-
-    // K, Q -> LDS: 32 windows of 64 16-byte units (4 rows each), dealt to the waves.
-    // Rows past the chunk's end repeat its last token: they meet beta = 0 or the causal
-    // mask only.
-    {
-        const char *kb = (const char *)(p.k + (int64_t)tok0 * p.k_st + g * p.k_sh);
-        const char *qb = (const char *)(p.q + (int64_t)tok0 * p.q_st + g * p.q_sh);
-        const uint32_t kst2 = (uint32_t)p.k_st * 2, qst2 = (uint32_t)p.q_st * 2;
+    struct Unit {
+        int c, g, h, tok0, len;
+    };
+    auto unit = [&](int u) {
+        Unit r;
+        const int grp = u / ngrp, hg = u % ngrp;
+        r.c = grp / p.HQK;
+        r.g = grp % p.HQK;
+        r.h = r.g * p.ratio + hg * VH + hv;
+        r.tok0 = p.chunk_tok0[r.c];
+        r.len = p.chunk_len[r.c];
+        return r;
+    };
+    // K or Q of a unit -> LDS: 16 windows of 64 16-byte units (4 rows each) per matrix,
+    // dealt to the waves. Rows past the chunk's end repeat its last token: they meet
+    // beta = 0 or the causal mask only.
+    auto copy = [&](const Unit &U, bool isq, u32x4 *dst) {
+        const char *base = isq ? (const char *)(p.q + (int64_t)U.tok0 * p.q_st + U.g * p.q_sh)
+                               : (const char *)(p.k + (int64_t)U.tok0 * p.k_st + U.g * p.k_sh);
+        const uint32_t st2 = isq ? qst2 : kst2;
 #pragma unroll
-        for (int i = 0; i < 8 / VH; ++i) {
-            const int win = wv + 4 * VH * i;
-            const int isq = win >= 16, b = win & 15;
+        for (int i = 0; i < 4 / VH; ++i) {
+            const int b = wv + 4 * VH * i;
             const int t = 4 * b + (l >> 4), cs = l & 15;
-            const uint32_t off = (uint32_t)min(t, len - 1) * (isq ? qst2 : kst2) + 16u * (cs ^ (t & 15));
-            dma16((isq ? qb : kb) + off, isq ? &Qs[64 * b] : &Ks[64 * b]);
+            dma16(base + (uint32_t)min(t, U.len - 1) * st2 + 16u * (cs ^ (t & 15)), &dst[64 * b]);
         }
-    }
-
+    };
     // Gates (gdn_decode/solution/triton/kernel.py:128-131); padding tokens: alpha = 1,
     // beta = 0. Cumulative decay in log2 units: every factor below is 2^(non-positive
     // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow).
-    if (w == 0) {
-        const int tl = tok0 + min(l, len - 1);
-        const float a_in = bf16_to_f32(p.a[(int64_t)tl * p.a_st + h * p.a_sh]);
-        const float b_in = bf16_to_f32(p.b[(int64_t)tl * p.b_st + h * p.b_sh]);
+    auto gate_in = [&](const Unit &U, float &a_in, float &b_in) {
+        const int tl = U.tok0 + min(l, U.len - 1);
+        a_in = bf16_to_f32(p.a[(int64_t)tl * p.a_st + U.h * p.a_sh]);
+        b_in = bf16_to_f32(p.b[(int64_t)tl * p.b_st + U.h * p.b_sh]);
+    };
+    auto gates = [&](const Unit &U, float a_in, float b_in, int buf) {
         float la = 0.f, bt = 0.f;
-        if (l < len) {
-            const float x = a_in + p.dt_bias[h * p.dt_s];
+        if (l < U.len) {
+            const float x = a_in + p.dt_bias[U.h * p.dt_s];
             const float sp = x > 20.f ? x : logf(1.f + expf(x));
-            la = -expf(p.A_log[h * p.A_log_s]) * sp;
+            la = -expf(p.A_log[U.h * p.A_log_s]) * sp;
             bt = 1.f / (1.f + expf(-b_in));
         }
         float L = la * 1.44269504088896340736f;
@@ -308,172 +319,241 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p)
                 L += y;
         }
         const float Lend = __shfl(L, 63, 64);
-        Ls[hv][l] = L;
-        Bs[hv][l] = bt;
-        LsT[hv][16 * (l >> 4) + 4 * (l & 3) + ((l >> 2) & 3)] = L;
-        float *gates = (float *)(rec + kRecGates);
+        sm.L[buf][hv][l] = L;
+        sm.B[buf][hv][l] = bt;
+        sm.LT[buf][hv][16 * (l >> 4) + 4 * (l & 3) + ((l >> 2) & 3)] = L;
+        char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
+        float *gts = (float *)(rec + kRecGates);
         const float gam = __builtin_amdgcn_exp2f(L);
-        gates[l] = gam;
-        gates[64 + l] = __builtin_amdgcn_exp2f(Lend - L);
-        gates[128 + l] = p.scale * gam;
+        gts[l] = gam;
+        gts[64 + l] = __builtin_amdgcn_exp2f(Lend - L);
+        gts[128 + l] = p.scale * gam;
         if (l == 0)
-            gates[192] = __builtin_amdgcn_exp2f(Lend);
+            gts[192] = __builtin_amdgcn_exp2f(Lend);
         if (l < 4)
             ((float *)(rec + kRecZero))[l] = 0.f;
-    }
-    dma_barrier();  // K, Q, L, beta visible to every wave
+    };
 
-    // MFMA operand: 16 rows (row(lr) of block b), k-chunk 4 ks + lg.
+    // MFMA operand: 16 rows, k-chunk 4 ks + lg.
     auto kop = [&](const u32x4 *M, int row, int ks) {
         return M[16 * row + ((4 * ks + lg) ^ (row & 15))];
     };
+    float (*Ms)[16] = sm.Ms[wv];
+    uint16_t *Tst = (uint16_t *)sm.Ms[wv];  // [2][256] bf16, after X_w is done with Ms
 
-    // P' row block w: lane (t = 16 w + lr, lg) holds columns 16 jb + 4 lg .. +3.
-    {
-        const int t = 16 * w + lr;
-        const float Lt = Ls[hv][t];
-        u32x4 qn[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            qn[ks] = kop(Qs, t, ks);
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-            if (jb > w)
-                break;
-            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Unit &U, const u32x4 *Kb, int buf, float &na, float &nb,
+                       const Unit &N, bool more) {
+        char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
+        const float *Ls = sm.L[buf][hv], *Bs = sm.B[buf][hv], *LsT = sm.LT[buf][hv];
+
+        // P' row block w: lane (t = 16 w + lr, lg) holds columns 16 jb + 4 lg .. +3.
+        {
+            const int t = 16 * w + lr;
+            const float Lt = Ls[t];
+            u32x4 qn[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
-                r = mfma_bf16(kop(Ks, 16 * jb + lr, ks), qn[ks], r);
-            const f32x4 Lj = *(const f32x4 *)&Ls[hv][16 * jb + 4 * lg];
-            float pv[4];
+                qn[ks] = kop(sm.Q, t, ks);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 16 * jb + 4 * lg + e;
-                pv[e] = j <= t ? p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * r[e] : 0.f;
+            for (int jb = 0; jb < 4; ++jb) {
+                if (jb > w)
+                    break;
+                f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    r = mfma_bf16(kop(Kb, 16 * jb + lr, ks), qn[ks], r);
+                const f32x4 Lj = *(const f32x4 *)&Ls[16 * jb + 4 * lg];
+                float pv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 16 * jb + 4 * lg + e;
+                    pv[e] = j <= t ? p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * r[e] : 0.f;
+                }
+                *(u32x2 *)(rec + kRecP + 2 * (tri_blk(w, jb) * kBlk + lr * 16 + 4 * lg)) =
+                    u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
             }
-            *(u32x2 *)(rec + kRecP + 2 * (tri_blk(w, jb) * kBlk + lr * 16 + 4 * lg)) =
-                u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
         }
-    }
 
-    // A blocks (i, m): lane (lr, lg) element e = A[16 i + pi(lr)][16 m + 4 e + lg].
-    f32x4 Ar[4][4];
+        // A blocks (i, m): lane (lr, lg) element e = A[16 i + pi(lr)][16 m + 4 e + lg].
+        f32x4 Ar[4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int m = 0; m <= i; ++m) {
-            Ar[i][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (i == m ? m != w : m < w)
+            for (int m = 0; m <= i; ++m) {
+                Ar[i][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (i == m ? m != w : m < w)
+                    continue;
+                f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    r = mfma_bf16(kop(Kb, 16 * m + pi16(lr), ks), kop(Kb, 16 * i + pi16(lr), ks), r);
+                const int t = 16 * i + pi16(lr);
+                const float Lt = Ls[t], btt = Bs[t];
+                const f32x4 Lm = *(const f32x4 *)&LsT[16 * m + 4 * lg];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 16 * m + 4 * e + lg;
+                    Ar[i][m][e] = j < t ? btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * r[e] : 0.f;
+                }
+            }
+
+        // X_w = (I + A_ww)^-1. Lane (lr, lg) holds row pi(lr), columns lg + 4 s (s = 0..3)
+        // of X; step m subtracts A[r][m] x (row m of X), row m being final (A is strictly
+        // lower, so rows r <= m see A[r][m] = 0). Row m sits in lane pi(m) of every 16-lane
+        // row, next to the same columns.
+        f32x4 xw;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i != w)
                 continue;
-            f32x4 r = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                r = mfma_bf16(kop(Ks, 16 * m + pi16(lr), ks), kop(Ks, 16 * i + pi16(lr), ks), r);
-            const int t = 16 * i + pi16(lr);
-            const float Lt = Ls[hv][t], btt = Bs[hv][t];
-            const f32x4 Lm = *(const f32x4 *)&LsT[hv][16 * m + 4 * lg];
+            for (int e = 0; e < 4; ++e)
+                Ms[pi16(lr)][4 * e + lg] = Ar[i][i][e];
+        }
+        {
+            float arow[16];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = 16 * m + 4 * e + lg;
-                Ar[i][m][e] = j < t ? btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * r[e] : 0.f;
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = *(const f32x4 *)&Ms[pi16(lr)][4 * q];
+                arow[4 * q] = v[0]; arow[4 * q + 1] = v[1]; arow[4 * q + 2] = v[2]; arow[4 * q + 3] = v[3];
             }
-        }
-
-    // X_w = (I + A_ww)^-1. Lane (lr, lg) holds row pi(lr), columns lg + 4 s (s = 0..3)
-    // of X; step m subtracts A[r][m] x (row m of X), row m being final (A is strictly
-    // lower, so rows r <= m see A[r][m] = 0). Row m sits in lane pi(m) of every 16-lane
-    // row, next to the same columns.
-    f32x4 xw;
+            float x[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (i != w)
-            continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            Ms[wv][pi16(lr)][4 * e + lg] = Ar[i][i][e];
-    }
-    {
-        float arow[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 v = *(const f32x4 *)&Ms[wv][pi16(lr)][4 * q];
-            arow[4 * q] = v[0]; arow[4 * q + 1] = v[1]; arow[4 * q + 2] = v[2]; arow[4 * q + 3] = v[3];
-        }
-        float x[4];
-#pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2)
-            x[s2] = pi16(lr) == lg + 4 * s2 ? 1.f : 0.f;
+            for (int s2 = 0; s2 < 4; ++s2)
+                x[s2] = pi16(lr) == lg + 4 * s2 ? 1.f : 0.f;
 #define GDN_SUBST_STEP(M)                                                         \
-        {                                                                         \
-            _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2)                      \
-                x[s2] = fmaf(-arow[M], row_bcast<4 * ((M) & 3) + ((M) >> 2)>(x[s2]), x[s2]); \
-        }
-        GDN_SUBST_STEP(0) GDN_SUBST_STEP(1) GDN_SUBST_STEP(2) GDN_SUBST_STEP(3)
-        GDN_SUBST_STEP(4) GDN_SUBST_STEP(5) GDN_SUBST_STEP(6) GDN_SUBST_STEP(7)
-        GDN_SUBST_STEP(8) GDN_SUBST_STEP(9) GDN_SUBST_STEP(10) GDN_SUBST_STEP(11)
-        GDN_SUBST_STEP(12) GDN_SUBST_STEP(13) GDN_SUBST_STEP(14)
+            {                                                                     \
+                _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2)                  \
+                    x[s2] = fmaf(-arow[M], row_bcast<4 * ((M) & 3) + ((M) >> 2)>(x[s2]), x[s2]); \
+            }
+            GDN_SUBST_STEP(0) GDN_SUBST_STEP(1) GDN_SUBST_STEP(2) GDN_SUBST_STEP(3)
+            GDN_SUBST_STEP(4) GDN_SUBST_STEP(5) GDN_SUBST_STEP(6) GDN_SUBST_STEP(7)
+            GDN_SUBST_STEP(8) GDN_SUBST_STEP(9) GDN_SUBST_STEP(10) GDN_SUBST_STEP(11)
+            GDN_SUBST_STEP(12) GDN_SUBST_STEP(13) GDN_SUBST_STEP(14)
 #undef GDN_SUBST_STEP
-        xw = f32x4{x[0], x[1], x[2], x[3]};
-    }
-    XA[hv][w][l] = xw;
-    // X_w in B-operand layout (lane (n, lg) element s = X[4 s + lg][n]) via this wave's scratch
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
-        Ms[wv][pi16(lr)][lg + 4 * s2] = xw[s2];
-    f32x4 TB[4];
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
-        TB[0][s2] = Ms[wv][4 * s2 + lg][lr];
-    lds_barrier();  // every X_i is in XA
-
-    // Column block w of T; TB[i] = T_(w+i),w in B-operand layout.
-#pragma unroll
-    for (int i = 1; i < 4; ++i) {
-        if (i + w > 3)
-            break;
-        f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int m = 0; m < i; ++m) {  // block m + w
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-#pragma unroll
-                for (int mm = 0; mm < 4; ++mm)
-                    if (ii == i + w && mm == m + w)
-#pragma unroll
-                        for (int s2 = 0; s2 < 4; ++s2)
-                            z = mfma_f32(Ar[ii][mm][s2], TB[m][s2], z);
+            xw = f32x4{x[0], x[1], x[2], x[3]};
         }
-        const f32x4 xa = XA[hv][i + w][l];
-        f32x4 t = {0.f, 0.f, 0.f, 0.f};
+        sm.XA[hv][w][l] = xw;
+        // X_w in B-operand layout (lane (n, lg) element s = X[4 s + lg][n]) via the scratch
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
-            t = mfma_f32(xa[s2], z[s2], t);
-        TB[i] = -t;
-    }
+            Ms[pi16(lr)][lg + 4 * s2] = xw[s2];
+        f32x4 TB[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            TB[0][s2] = Ms[4 * s2 + lg][lr];
+        lds_barrier();  // every X_i is in XA; every wave is done with Q
+        if (more)
+            copy(N, true, sm.Q);
 
-    // T' = T diag(beta) -> record (bf16 hi / lo, block layout), one block at a time
-    // through this wave's staging area (B layout -> row-major 16-byte units).
-    const float bcol = Bs[hv][16 * w + lr];
+        // Column block w of T; TB[i] = T_(w+i),w in B-operand layout.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (i + w > 3)
-            break;
+        for (int i = 1; i < 4; ++i) {
+            if (i + w > 3)
+                break;
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) {
-            const float v = TB[i][s2] * bcol;
-            const uint32_t hi = f32_to_bf16(v);
-            const uint32_t lo = f32_to_bf16(v - bf16_to_f32(hi));
-            Tst[wv][0][(4 * s2 + lg) * 16 + lr] = (uint16_t)hi;
-            Tst[wv][1][(4 * s2 + lg) * 16 + lr] = (uint16_t)lo;
+            for (int m = 0; m < i; ++m) {  // block m + w
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+                    for (int mm = 0; mm < 4; ++mm)
+                        if (ii == i + w && mm == m + w)
+#pragma unroll
+                            for (int s2 = 0; s2 < 4; ++s2)
+                                z = mfma_f32(Ar[ii][mm][s2], TB[m][s2], z);
+            }
+            const f32x4 xa = sm.XA[hv][i + w][l];
+            f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+                t = mfma_f32(xa[s2], z[s2], t);
+            TB[i] = -t;
         }
-        const int half = l >> 5, u = l & 31;
-        const u32x4 unit = *(const u32x4 *)&Tst[wv][half][8 * u];
-        *(u32x4 *)(rec + (half ? kRecTlo : kRecThi) + tri_blk(i + w, w) * 512 + 16 * u) = unit;
+
+        // T' = T diag(beta) -> record (bf16 hi / lo, block layout), one block at a time
+        // through this wave's staging area (B layout -> row-major 16-byte units).
+        const float bcol = Bs[16 * w + lr];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i + w > 3)
+                break;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const float v = TB[i][s2] * bcol;
+                const uint32_t hi = f32_to_bf16(v);
+                const uint32_t lo = f32_to_bf16(v - bf16_to_f32(hi));
+                Tst[(4 * s2 + lg) * 16 + lr] = (uint16_t)hi;
+                Tst[256 + (4 * s2 + lg) * 16 + lr] = (uint16_t)lo;
+            }
+            const int half = l >> 5, u = l & 31;
+            const u32x4 unit_v = *(const u32x4 *)&Tst[256 * half + 8 * u];
+            *(u32x4 *)(rec + (half ? kRecTlo : kRecThi) + tri_blk(i + w, w) * 512 + 16 * u) = unit_v;
+        }
+
+        // next unit's gates (its inputs were loaded one unit ago)
+        if (more && w == 0)
+            gates(N, na, nb, buf ^ 1);
+    };
+
+    int u = blockIdx.x;
+    if (u >= nunits)
+        return;
+    Unit U = unit(u);
+    float a_in = 0.f, b_in = 0.f;
+    copy(U, false, sm.K[0]);
+    copy(U, true, sm.Q);
+    if (w == 0) {
+        gate_in(U, a_in, b_in);
+        gates(U, a_in, b_in, 0);
+    }
+    for (;;) {
+        // even step: K in sm.K[0], gates in buffer 0
+        int un = u + gridDim.x;
+        bool more = un < nunits;
+        Unit N = more ? unit(un) : U;
+        dma_barrier();
+        if (more) {
+            copy(N, false, sm.K[1]);
+            if (w == 0)
+                gate_in(N, a_in, b_in);
+        }
+        compute(U, sm.K[0], 0, a_in, b_in, N, more);
+        if (!more)
+            break;
+        u = un;
+        U = N;
+        // odd step: K in sm.K[1], gates in buffer 1
+        un = u + gridDim.x;
+        more = un < nunits;
+        N = more ? unit(un) : U;
+        dma_barrier();
+        if (more) {
+            copy(N, false, sm.K[0]);
+            if (w == 0)
+                gate_in(N, a_in, b_in);
+        }
+        compute(U, sm.K[1], 1, a_in, b_in, N, more);
+        if (!more)
+            break;
+        u = un;
+        U = N;
     }
 }
 
-__global__ __launch_bounds__(256) void gdn_prefill_prep1_kernel(PrepArgs p) { prep_body<1>(p); }
-__global__ __launch_bounds__(512) void gdn_prefill_prep2_kernel(PrepArgs p) { prep_body<2>(p); }
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gdn_prefill_prep1_kernel(PrepArgs p)
+{
+    __shared__ PrepSmem<1> sm;
+    prep_body<1>(p, sm);
+}
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void
+gdn_prefill_prep2_kernel(PrepArgs p)
+{
+    __shared__ PrepSmem<2> sm;
+    prep_body<2>(p, sm);
+}
 
 // ------------------------------------------------------------------------- scan
 struct ScanArgs {
@@ -907,6 +987,26 @@ Layout layout(int64_t T, int64_t N, int64_t HV)
 
 bool aligned(const void *p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
+// Compute units of the device that owns the stream (the current device when the
+// stream is the null stream); 256 if the runtime cannot tell.
+int num_cus(hipStream_t st)
+{
+    int dev = -1;
+    if (st == nullptr || hipStreamGetDevice(st, &dev) != hipSuccess)
+        if (hipGetDevice(&dev) != hipSuccess)
+            return 256;
+    static int cached[64] = {0};
+    if (dev < 0 || dev >= 64)
+        return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 }  // namespace
 
 extern "C" int64_t gdn_prefill_workspace_size(int32_t total_tokens, int32_t num_seqs,
@@ -1031,10 +1131,10 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         qa.HV = HV;
         qa.ratio = ratio;
         qa.scale = p->scale;
-        // one workgroup per (chunk, q/k head, pair of v-heads) when the ratio is even
+        // persistent: two workgroups per CU walk the (chunk, q/k head, v-head pair) units
         const int vh = ratio % 2 == 0 ? 2 : 1;
-        const int64_t units = L.nc * HQK;  // (chunk, q/k head) groups
-        const int64_t blocks = 8 * (int64_t)(ratio / vh) * ((units + 7) / 8);
+        const int64_t units = L.nc * HQK * (ratio / vh);
+        const int64_t blocks = std::min<int64_t>(units, 2 * (int64_t)num_cus(st));
         if (blocks > 0x7fffffff)
             return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
         if (vh == 2)
