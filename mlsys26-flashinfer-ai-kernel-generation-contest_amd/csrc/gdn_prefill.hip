@@ -225,12 +225,14 @@ struct PrepArgs {
 // layout of the next v_mfma_f32_16x16x4_f32 (k-slice i, lane (n, g) supplies k = 4 i + g).
 __device__ __forceinline__ int pi16(int m) { return 4 * (m & 3) + (m >> 2); }
 
-// Broadcast lane K of every 16-lane row (DPP row_newbcast).
-template <int K>
-__device__ __forceinline__ float row_bcast(float x)
-{
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x150 + K, 0xF, 0xF, false));
-}
+// acc += coef * (acc of lane K in this 16-lane row): one v_fmac_f32 with a DPP row_newbcast
+// source. Callers keep >= 2 other VALU instructions between the last write of acc and
+// this read (the DPP read-after-write hazard); the first use in a chain is preceded by
+// s_nop 1.
+#define GDN_FMAC_BCAST(acc, coef, K)                                                     \
+    asm volatile("v_fmac_f32_dpp %0, %0, %1 row_newbcast:" #K " row_mask:0xf bank_mask:0xf" \
+                 : "+v"(acc)                                                              \
+                 : "v"(coef))
 
 // Work unit: (chunk, q/k head, group of VH v-heads). A persistent workgroup of 4 VH waves
 // walks units u = blockIdx.x, + gridDim.x, ...; wave (hv, w) = v-head hv of the group,
@@ -238,10 +240,10 @@ __device__ __forceinline__ float row_bcast(float x)
 // unit's copies and gate inputs in flight while this one computes) and serve every
 // v-head of the group. Per unit, wave (hv, w):
 //   * writes P' row block w: P'[t, j] = scale 2^(L_t - L_j) q_t . k_j, j <= t;
-//   * forms the A blocks it needs, A[t, j] = beta_t 2^(L_t - L_j) k_t . k_j (j < t):
-//     (w, w) and (i, m) for w <= m < i;
+//   * forms A column block w, A[t, j] = beta_t 2^(L_t - L_j) k_t . k_j (j < t): the
+//     diagonal block stays in registers, blocks (i > w, w) go to LDS for every wave;
 //   * inverts X_w = (I + A_ww)^-1 by forward substitution (DPP broadcasts);
-//   * after a barrier (all X_i published): column block w of T = (I + A)^-1,
+//   * after a barrier (all X_i and A blocks published): column block w of T = (I + A)^-1,
 //       T_ww = X_w,  T_iw = -X_i sum_{m=w}^{i-1} A_im T_mw  (i > w),
 //     on fp32 MFMA with every operand in registers, and writes T' = T diag(beta);
 // wave (hv, 0) also computes the next unit's gates and cumulative log2 decay L.
@@ -254,7 +256,8 @@ struct PrepSmem {
     float LT[2][VH][64];  // L of token 16 b + 4 i + g at 16 b + 4 g + i
     float B[2][VH][64];   // beta by token
     f32x4 XA[VH][4][64];  // X_w in A-operand layout, by lane
-    float Ms[4 * VH][16][16];  // per wave: A_ww rows, X_w, then T' staging (bf16)
+    f32x4 AO[VH][6][64];  // off-diagonal A_im (m < i) in A-operand layout, by lane; i(i-1)/2 + m
+    float Ms[4 * VH][16][16];  // per wave: -A_ww rows, X_w, then T' staging
 };
 
 template <int VH>
@@ -339,7 +342,6 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         return M[16 * row + ((4 * ks + lg) ^ (row & 15))];
     };
     float (*Ms)[16] = sm.Ms[wv];
-    uint16_t *Tst = (uint16_t *)sm.Ms[wv];  // [2][256] bf16, after X_w is done with Ms
 
     auto compute = [&](const Unit &U, const u32x4 *Kb, int buf, float &na, float &nb,
                        const Unit &N, bool more) {
@@ -367,21 +369,21 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = 16 * jb + 4 * lg + e;
-                    pv[e] = j <= t ? p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * r[e] : 0.f;
+                    const float v = p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * r[e];
+                    pv[e] = (jb < w || j <= t) ? v : 0.f;  // only the diagonal block is masked
                 }
                 *(u32x2 *)(rec + kRecP + 2 * (tri_blk(w, jb) * kBlk + lr * 16 + 4 * lg)) =
                     u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
             }
         }
 
-        // A blocks (i, m): lane (lr, lg) element e = A[16 i + pi(lr)][16 m + 4 e + lg].
-        f32x4 Ar[4][4];
+        // A column block w: lane (lr, lg) element e = A[16 i + pi(lr)][16 w + 4 e + lg].
+        f32x4 Aww = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int m = 0; m <= i; ++m) {
-                Ar[i][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (i == m ? m != w : m < w)
+            for (int m = 0; m <= i; ++m) {  // only m == w runs; unrolled so blocks index statically
+                if (m != w)
                     continue;
                 f32x4 r = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -390,11 +392,17 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 const int t = 16 * i + pi16(lr);
                 const float Lt = Ls[t], btt = Bs[t];
                 const f32x4 Lm = *(const f32x4 *)&LsT[16 * m + 4 * lg];
+                f32x4 av;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = 16 * m + 4 * e + lg;
-                    Ar[i][m][e] = j < t ? btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * r[e] : 0.f;
+                    const float v = btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * r[e];
+                    av[e] = (m < i || j < t) ? v : 0.f;  // only the diagonal block is masked
                 }
+                if (i == m)
+                    Aww = av;
+                else
+                    sm.AO[hv][i * (i - 1) / 2 + m][l] = av;
             }
 
         // X_w = (I + A_ww)^-1. Lane (lr, lg) holds row pi(lr), columns lg + 4 s (s = 0..3)
@@ -403,13 +411,8 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         // row, next to the same columns.
         f32x4 xw;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (i != w)
-                continue;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                Ms[pi16(lr)][4 * e + lg] = Ar[i][i][e];
-        }
+        for (int e = 0; e < 4; ++e)
+            Ms[pi16(lr)][4 * e + lg] = -Aww[e];
         {
             float arow[16];
 #pragma unroll
@@ -421,15 +424,15 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2)
                 x[s2] = pi16(lr) == lg + 4 * s2 ? 1.f : 0.f;
-#define GDN_SUBST_STEP(M)                                                         \
-            {                                                                     \
-                _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2)                  \
-                    x[s2] = fmaf(-arow[M], row_bcast<4 * ((M) & 3) + ((M) >> 2)>(x[s2]), x[s2]); \
-            }
-            GDN_SUBST_STEP(0) GDN_SUBST_STEP(1) GDN_SUBST_STEP(2) GDN_SUBST_STEP(3)
-            GDN_SUBST_STEP(4) GDN_SUBST_STEP(5) GDN_SUBST_STEP(6) GDN_SUBST_STEP(7)
-            GDN_SUBST_STEP(8) GDN_SUBST_STEP(9) GDN_SUBST_STEP(10) GDN_SUBST_STEP(11)
-            GDN_SUBST_STEP(12) GDN_SUBST_STEP(13) GDN_SUBST_STEP(14)
+            asm volatile("s_nop 1" ::: "memory");
+            // arow holds -A; the broadcast lane of step M is pi(M)
+#define GDN_SUBST_STEP(M, K)                                                      \
+            GDN_FMAC_BCAST(x[0], arow[M], K); GDN_FMAC_BCAST(x[1], arow[M], K);   \
+            GDN_FMAC_BCAST(x[2], arow[M], K); GDN_FMAC_BCAST(x[3], arow[M], K);
+            GDN_SUBST_STEP(0, 0) GDN_SUBST_STEP(1, 4) GDN_SUBST_STEP(2, 8) GDN_SUBST_STEP(3, 12)
+            GDN_SUBST_STEP(4, 1) GDN_SUBST_STEP(5, 5) GDN_SUBST_STEP(6, 9) GDN_SUBST_STEP(7, 13)
+            GDN_SUBST_STEP(8, 2) GDN_SUBST_STEP(9, 6) GDN_SUBST_STEP(10, 10) GDN_SUBST_STEP(11, 14)
+            GDN_SUBST_STEP(12, 3) GDN_SUBST_STEP(13, 7) GDN_SUBST_STEP(14, 11)
 #undef GDN_SUBST_STEP
             xw = f32x4{x[0], x[1], x[2], x[3]};
         }
@@ -442,7 +445,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
             TB[0][s2] = Ms[4 * s2 + lg][lr];
-        lds_barrier();  // every X_i is in XA; every wave is done with Q
+        lds_barrier();  // every X_i is in XA, every A_im in AO; every wave is done with Q
         if (more)
             copy(N, true, sm.Q);
 
@@ -453,15 +456,12 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 break;
             f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int m = 0; m < i; ++m) {  // block m + w
+            for (int m = 0; m < i; ++m) {  // A block (i + w, m + w)
+                const int ii = i + w, mm = m + w;
+                const f32x4 a = sm.AO[hv][ii * (ii - 1) / 2 + mm][l];
 #pragma unroll
-                for (int ii = 0; ii < 4; ++ii)
-#pragma unroll
-                    for (int mm = 0; mm < 4; ++mm)
-                        if (ii == i + w && mm == m + w)
-#pragma unroll
-                            for (int s2 = 0; s2 < 4; ++s2)
-                                z = mfma_f32(Ar[ii][mm][s2], TB[m][s2], z);
+                for (int s2 = 0; s2 < 4; ++s2)
+                    z = mfma_f32(a[s2], TB[m][s2], z);
             }
             const f32x4 xa = sm.XA[hv][i + w][l];
             f32x4 t = {0.f, 0.f, 0.f, 0.f};
@@ -472,23 +472,23 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         }
 
         // T' = T diag(beta) -> record (bf16 hi / lo, block layout), one block at a time
-        // through this wave's staging area (B layout -> row-major 16-byte units).
+        // through this wave's fp32 staging tile: lane (row l / 4, columns 4 (l % 4) .. +3)
+        // splits its four values and stores 8 bytes of hi and 8 of lo.
         const float bcol = Bs[16 * w + lr];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             if (i + w > 3)
                 break;
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const float v = TB[i][s2] * bcol;
-                const uint32_t hi = f32_to_bf16(v);
-                const uint32_t lo = f32_to_bf16(v - bf16_to_f32(hi));
-                Tst[(4 * s2 + lg) * 16 + lr] = (uint16_t)hi;
-                Tst[256 + (4 * s2 + lg) * 16 + lr] = (uint16_t)lo;
-            }
-            const int half = l >> 5, u = l & 31;
-            const u32x4 unit_v = *(const u32x4 *)&Tst[256 * half + 8 * u];
-            *(u32x4 *)(rec + (half ? kRecTlo : kRecThi) + tri_blk(i + w, w) * 512 + 16 * u) = unit_v;
+            for (int s2 = 0; s2 < 4; ++s2)
+                Ms[4 * s2 + lg][lr] = TB[i][s2] * bcol;
+            const f32x4 v = *(const f32x4 *)&Ms[l >> 2][4 * (l & 3)];
+            uint32_t h01, l01, h23, l23;
+            split_bf16x2(v[0], v[1], h01, l01);
+            split_bf16x2(v[2], v[3], h23, l23);
+            const int off = tri_blk(i + w, w) * 512 + (l >> 2) * 32 + 8 * (l & 3);
+            *(u32x2 *)(rec + kRecThi + off) = u32x2{h01, h23};
+            *(u32x2 *)(rec + kRecTlo + off) = u32x2{l01, l23};
         }
 
         // next unit's gates (its inputs were loaded one unit ago)
