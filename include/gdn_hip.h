@@ -48,14 +48,17 @@ const char *gdn_last_error(void);
  *   state      f32  [B, HV, D, D] (k-last: [.., v, k]); NULL = zero initial state
  *   new_state  f32  [B, HV, D, D]; may alias state exactly (in-place update)
  *   A_log, dt_bias  f32 [HV]            a, b       bf16 [B, T, HV]
- * Constraints: T == 1, D == 128, HV % HQK == 0; state / new_state 16-byte aligned
+ * Constraints: T >= 1, D == 128, HV % HQK == 0; state / new_state 16-byte aligned
  * with v/h/b strides multiples of 4; q/k/v/output 8-byte aligned with outer strides
  * multiples of 4.
+ * T > 1: every token is one step from the input state, as each per-token program of
+ * gdn_decode/solution/triton/kernel.py:110-118,146-147 loads it; new_state receives
+ * the last token's update, and must not alias state (GDN_EINVAL).
  */
 typedef struct gdn_decode_params {
     int32_t struct_size; /* = sizeof(gdn_decode_params) */
     int32_t batch;       /* B */
-    int32_t seq_len;     /* T (must be 1) */
+    int32_t seq_len;     /* T (1 in the reference's workloads) */
     int32_t num_qk_heads;
     int32_t num_v_heads;
     int32_t head_size;   /* D */

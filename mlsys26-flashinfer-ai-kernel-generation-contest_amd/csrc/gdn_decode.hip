@@ -10,6 +10,11 @@
 // (gdn_decode/solution/triton/kernel.py:120-131,165-170,216-218) with the readout
 // S' q expanded so that it needs no second sweep over S'.
 //
+// seq_len T > 1 follows the reference kernel, whose programs (b, h, tile, t) each start
+// from the input state (gdn_decode/solution/triton/kernel.py:117-118,146-147): token t's
+// output is one decode step from the input state. The reference lets every token store
+// new_state; here only token T - 1 stores it, so the result is deterministic.
+//
 // Thread mapping (default): a workgroup of 256 lanes covers 32 state rows; each
 // row is spread over 8 consecutive lanes and each lane owns 16 columns as four
 // float4 at columns 4s + 32j (s = lane % 8, j = 0..3), so one load instruction
@@ -29,13 +34,13 @@ struct DecodeArgs {
     const bf16_t *b;
     bf16_t *out;
     float *new_state;
-    int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh;
+    int64_t q_sb, q_st, q_sh, k_sb, k_st, k_sh, v_sb, v_st, v_sh;
     int64_t st_sb, st_sh, st_sv;
-    int64_t a_sb, a_sh, b_sb, b_sh;
-    int64_t o_sb, o_sh;
+    int64_t a_sb, a_st, a_sh, b_sb, b_st, b_sh;
+    int64_t o_sb, o_st, o_sh;
     int64_t ns_sb, ns_sh, ns_sv;
     int64_t A_log_s, dt_s;
-    int HV, ratio;
+    int B, T, HV, ratio;
     float scale;
 };
 
@@ -81,7 +86,9 @@ __global__ __launch_bounds__(THREADS) void gdn_decode_kernel(DecodeArgs p)
     const int vt = bid % kNVT;
     const int bh = bid / kNVT;
     const int h = bh % p.HV;
-    const int bi = bh / p.HV;
+    const int bt = bh / p.HV;
+    const int bi = bt % p.B;
+    const int t = bt / p.B;  // token; every token starts from the input state
     const int g = h / p.ratio;  // GVA: q/k head of this v-head (kernel.py:120)
     const int tid = threadIdx.x;
     const int s = tid % LPR;
@@ -92,12 +99,12 @@ __global__ __launch_bounds__(THREADS) void gdn_decode_kernel(DecodeArgs p)
     // Load order matters: vector loads return in issue order, so the few small loads
     // (gates, k, q, v) go first and the state stream right after; the gate math then
     // waits only for the small ones while the state is still in flight.
-    const uint32_t a_raw = p.a[bi * p.a_sb + h * p.a_sh];
-    const uint32_t b_raw = p.b[bi * p.b_sb + h * p.b_sh];
+    const uint32_t a_raw = p.a[bi * p.a_sb + t * p.a_st + h * p.a_sh];
+    const uint32_t b_raw = p.b[bi * p.b_sb + t * p.b_st + h * p.b_sh];
     u32x2 kraw[kNV4], qraw[kNV4];
     {
-        const bf16_t *kp = p.k + bi * p.k_sb + g * p.k_sh + 4 * s;
-        const bf16_t *qp = p.q + bi * p.q_sb + g * p.q_sh + 4 * s;
+        const bf16_t *kp = p.k + bi * p.k_sb + t * p.k_st + g * p.k_sh + 4 * s;
+        const bf16_t *qp = p.q + bi * p.q_sb + t * p.q_st + g * p.q_sh + 4 * s;
 #pragma unroll
         for (int j = 0; j < kNV4; ++j) {
             kraw[j] = *reinterpret_cast<const u32x2 *>(kp + 4 * LPR * j);
@@ -107,7 +114,7 @@ __global__ __launch_bounds__(THREADS) void gdn_decode_kernel(DecodeArgs p)
     uint32_t vraw[RPT];
 #pragma unroll
     for (int r = 0; r < RPT; ++r)
-        vraw[r] = p.v[bi * p.v_sb + h * p.v_sh + v0 + rg + kRowsPerPass * r];
+        vraw[r] = p.v[bi * p.v_sb + t * p.v_st + h * p.v_sh + v0 + rg + kRowsPerPass * r];
     __builtin_amdgcn_sched_barrier(0);
 
     f32x4 S[RPT][kNV4];
@@ -157,7 +164,8 @@ __global__ __launch_bounds__(THREADS) void gdn_decode_kernel(DecodeArgs p)
     kq = row_sum<LPR>(kq);
 
     float *nbase = p.new_state + bi * p.ns_sb + h * p.ns_sh;
-    bf16_t *obase = p.out + bi * p.o_sb + h * p.o_sh;
+    bf16_t *obase = p.out + bi * p.o_sb + t * p.o_st + h * p.o_sh;
+    const bool store_state = t == p.T - 1;
     const float omb = 1.f - beta;
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
@@ -180,15 +188,17 @@ __global__ __launch_bounds__(THREADS) void gdn_decode_kernel(DecodeArgs p)
         const float d = nv - u;                      // kernel.py:168
         const float o = fmaf(alpha, sq, d * kq);     // (alpha S + d k^T) q
         float *nrow = nbase + (int64_t)row * p.ns_sv + 4 * s;
+        if (store_state) {
 #pragma unroll
-        for (int j = 0; j < kNV4; ++j) {
-            f32x4 w;
+            for (int j = 0; j < kNV4; ++j) {
+                f32x4 w;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float sv = HAS_STATE ? S[r][j][e] : 0.f;
-                w[e] = fmaf(alpha, sv, d * kk[4 * j + e]);  // kernel.py:169
+                for (int e = 0; e < 4; ++e) {
+                    const float sv = HAS_STATE ? S[r][j][e] : 0.f;
+                    w[e] = fmaf(alpha, sv, d * kk[4 * j + e]);  // kernel.py:169
+                }
+                st4<NT>(nrow + 4 * LPR * j, w);
             }
-            st4<NT>(nrow + 4 * LPR * j, w);
         }
         if (s == 0)
             obase[row] = (bf16_t)f32_to_bf16(p.scale * o);  // kernel.py:216-218
@@ -232,8 +242,8 @@ extern "C" int gdn_decode_launch(const gdn_decode_params *p, void *stream)
         return gdn_set_error(GDN_EINVAL, "gdn_decode: bad sizes B=%d HQK=%d HV=%d", B, HQK, HV);
     if (D != 128)
         return gdn_set_error(GDN_EINVAL, "gdn_decode: head_size %d unsupported (128 only)", D);
-    if (T != 1)
-        return gdn_set_error(GDN_EINVAL, "gdn_decode: seq_len %d unsupported (1 only)", T);
+    if (T < 1)
+        return gdn_set_error(GDN_EINVAL, "gdn_decode: seq_len %d must be >= 1", T);
     if (B == 0)
         return GDN_OK;
     if (!p->q || !p->k || !p->v || !p->A_log || !p->a || !p->dt_bias || !p->b || !p->output ||
@@ -257,6 +267,9 @@ extern "C" int gdn_decode_launch(const gdn_decode_params *p, void *stream)
     if (p->state && (const void *)p->state != (const void *)p->new_state) {
         // Distinct buffers are fine; identical buffers must also share strides.
     } else if (p->state) {
+        if (T > 1)
+            return gdn_set_error(GDN_EINVAL, "gdn_decode: seq_len > 1 reads the input state "
+                                 "for every token; new_state must not alias state");
         for (int i = 0; i < 4; ++i)
             if (p->state_stride[i] != p->new_state_stride[i])
                 return gdn_set_error(GDN_ELAYOUT,
@@ -275,30 +288,38 @@ extern "C" int gdn_decode_launch(const gdn_decode_params *p, void *stream)
     a.out = (gdn::bf16_t *)p->output;
     a.new_state = p->new_state;
     a.q_sb = p->q_stride[0];
+    a.q_st = p->q_stride[1];
     a.q_sh = p->q_stride[2];
     a.k_sb = p->k_stride[0];
+    a.k_st = p->k_stride[1];
     a.k_sh = p->k_stride[2];
     a.v_sb = p->v_stride[0];
+    a.v_st = p->v_stride[1];
     a.v_sh = p->v_stride[2];
     a.st_sb = p->state_stride[0];
     a.st_sh = p->state_stride[1];
     a.st_sv = p->state_stride[2];
     a.a_sb = p->a_stride[0];
+    a.a_st = p->a_stride[1];
     a.a_sh = p->a_stride[2];
     a.b_sb = p->b_stride[0];
+    a.b_st = p->b_stride[1];
     a.b_sh = p->b_stride[2];
     a.o_sb = p->output_stride[0];
+    a.o_st = p->output_stride[1];
     a.o_sh = p->output_stride[2];
     a.ns_sb = p->new_state_stride[0];
     a.ns_sh = p->new_state_stride[1];
     a.ns_sv = p->new_state_stride[2];
     a.A_log_s = p->A_log_stride;
     a.dt_s = p->dt_bias_stride;
+    a.B = B;
+    a.T = T;
     a.HV = HV;
     a.ratio = HV / HQK;
     a.scale = p->scale;
 
-    const int64_t nstates = (int64_t)B * HV;
+    const int64_t nstates = (int64_t)B * T * HV;  // one grid slice per token
     hipStream_t st = (hipStream_t)stream;
     // variant (tuning sweeps): workgroup size x lanes per state row x rows per lane
     // x non-temporal hint; 0 is the default.

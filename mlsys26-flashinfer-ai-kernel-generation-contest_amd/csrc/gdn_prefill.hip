@@ -44,8 +44,6 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c)
 
 constexpr int kC = 64;   // chunk length
 constexpr int kDK = 128; // head size
-constexpr int kLdK = 136; // padded LDS row (bf16) for 64 x 128 tiles
-constexpr int kLdT = 72;  // padded LDS row (bf16) for 16 x 64 tiles
 
 // Per (chunk, v-head) record in the workspace. 64x64 lower-triangular matrices are
 // stored as their 10 lower 16x16 blocks, block (i, j <= i) at index i(i+1)/2 + j,

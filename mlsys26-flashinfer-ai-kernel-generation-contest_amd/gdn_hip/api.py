@@ -109,9 +109,8 @@ def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_sta
         raise ValueError(f"head_size {D} unsupported: the kernels are built for D={_D}")
     if HV % HQK != 0:
         raise ValueError(f"num_v_heads ({HV}) must be a multiple of num_q_heads ({HQK})")
-    if T != 1:
-        raise ValueError(f"gdn_decode handles seq_len == 1 (got {T}); use gdn_prefill for "
-                         "multi-token sequences")
+    if T < 1:
+        raise ValueError(f"seq_len must be >= 1 (got {T})")
     if state is not None:
         _need_tensor("state", state, torch.float32, 4)
         _need_shape("state", state, (B, HV, D, D))
@@ -155,7 +154,10 @@ def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_sta
     if not _layout_ok(new_state, *st_ok):
         ns_ = torch.empty((B, HV, D, D), dtype=torch.float32, device=dev)
         copy_back.append((new_state, ns_))
-    if st_ is not None and st_.data_ptr() == ns_.data_ptr() and st_.stride() != ns_.stride():
+    # in place needs identical strides, and seq_len 1: with T > 1 every token reads the
+    # input state while the last one writes new_state
+    if st_ is not None and st_.data_ptr() == ns_.data_ptr() and (
+            T > 1 or st_.stride() != ns_.stride()):
         st_ = st_.clone()
 
     P = _lib.DecodeParams()
@@ -180,12 +182,16 @@ def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_sta
 
 @torch.no_grad()
 def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale, output=None, new_state=None):
-    """Gated DeltaNet single-token decode (k-last fp32 state).
+    """Gated DeltaNet decode (k-last fp32 state).
 
-    q, k: bf16 [B, 1, HQK, D]; v: bf16 [B, 1, HV, D]; state: fp32 [B, HV, D, D] or None
-    (zeros); A_log, dt_bias: fp32 [HV]; a, b: bf16 [B, 1, HV]; scale: float (None/0 ->
-    1/sqrt(D)). Returns (output bf16 [B, 1, HV, D], new_state fp32 [B, HV, D, D]);
+    q, k: bf16 [B, T, HQK, D]; v: bf16 [B, T, HV, D]; state: fp32 [B, HV, D, D] or None
+    (zeros); A_log, dt_bias: fp32 [HV]; a, b: bf16 [B, T, HV]; scale: float (None/0 ->
+    1/sqrt(D)). Returns (output bf16 [B, T, HV, D], new_state fp32 [B, HV, D, D]);
     ``new_state`` may be ``state`` itself (in-place update).
+    T is 1 in the reference's workloads. For T > 1 each token is one step from the input
+    state, as the reference kernel's per-token programs compute it
+    (gdn_decode/solution/triton/kernel.py:117-118,146-147); new_state is the last token's
+    update (the reference lets every token store it, in no fixed order).
     Mirrors gdn_decode/solution/triton/kernel.py:221-272 (defaults at :238-247).
     """
     P, output, new_state, copy_back, _keep = _decode_marshal(

@@ -102,14 +102,14 @@ class PrefillInputs:
 
 
 def decode_inputs(batch, hqk=HQK, hv=HV, d=D, seed=0, with_state=True, gates="strong",
-                  state_std=0.02):
+                  state_std=0.02, seq_len=1):
     g = _gen(seed)
-    q = _unit_bf16((batch, 1, hqk, d), g)
-    k = _unit_bf16((batch, 1, hqk, d), g)
-    v = torch.randn((batch, 1, hv, d), generator=g).to(torch.bfloat16)
+    q = _unit_bf16((batch, seq_len, hqk, d), g)
+    k = _unit_bf16((batch, seq_len, hqk, d), g)
+    v = torch.randn((batch, seq_len, hv, d), generator=g).to(torch.bfloat16)
     A_log, dt_bias = _gate_params(hv, g, gates)
-    a = torch.randn((batch, 1, hv), generator=g).to(torch.bfloat16)
-    b = torch.randn((batch, 1, hv), generator=g).to(torch.bfloat16)
+    a = torch.randn((batch, seq_len, hv), generator=g).to(torch.bfloat16)
+    b = torch.randn((batch, seq_len, hv), generator=g).to(torch.bfloat16)
     state = (torch.randn((batch, hv, d, d), generator=g) * state_std).float() if with_state \
         else None
     return DecodeInputs(q, k, v, state, A_log, a, dt_bias, b, 1.0 / math.sqrt(d))

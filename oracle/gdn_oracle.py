@@ -125,14 +125,25 @@ def _default_scale(scale, D):
 
 # ----------------------------------------------------------------------------- C oracle
 def decode(q, k, v, state, A_log, a, dt_bias, b, scale, precision: str = "f64", threads: int = 0):
-    """Decode oracle. Shapes: q,k [B,1,HQK,D], v [B,1,HV,D], state [B,HV,D,D] or None,
-    A_log/dt_bias [HV], a/b [B,1,HV]. Returns (out [B,1,HV,D], new_state [B,HV,D,D]) in
-    float64 or float32 (unrounded; the reference stores out as bf16)."""
+    """Decode oracle. Shapes: q,k [B,T,HQK,D], v [B,T,HV,D], state [B,HV,D,D] or None,
+    A_log/dt_bias [HV], a/b [B,T,HV]. Returns (out [B,T,HV,D], new_state [B,HV,D,D]) in
+    float64 or float32 (unrounded; the reference stores out as bf16).
+
+    T > 1: the reference launches one program per (token, value tile) and each loads the
+    same input state (gdn_decode/solution/triton/kernel.py:110-118,146-147), so token t's
+    output is one step from the input state; new_state is token T-1's update."""
     q, k, v, a, b = (_u16(x) for x in (q, k, v, a, b))
     A_log, dt_bias, state = _f32(A_log), _f32(dt_bias), _f32(state)
     B, T, HQK, D = q.shape
-    if T != 1:
-        raise ValueError("decode oracle handles seq_len == 1")
+    if T < 1:
+        raise ValueError("decode oracle needs seq_len >= 1")
+    if T > 1:
+        outs = []
+        for t in range(T):
+            o_t, ns = decode(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], state, A_log,
+                             a[:, t:t + 1], dt_bias, b[:, t:t + 1], scale, precision, threads)
+            outs.append(o_t)
+        return np.concatenate(outs, axis=1), ns
     HV = v.shape[2]
     scale = _default_scale(scale, D)
     dt = np.float64 if precision == "f64" else np.float32

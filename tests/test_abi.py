@@ -81,7 +81,7 @@ def test_decode_rejects_bad_params_without_launch():
     P.batch, P.seq_len, P.num_qk_heads, P.num_v_heads, P.head_size = 2, 1, 16, 32, 64
     assert lib.gdn_decode_launch(ctypes.byref(P), None) == _lib.GDN_EINVAL
     assert "head_size" in _lib.last_error()
-    P.head_size, P.seq_len = 128, 2
+    P.head_size, P.seq_len = 128, 0
     assert lib.gdn_decode_launch(ctypes.byref(P), None) == _lib.GDN_EINVAL
     assert "seq_len" in _lib.last_error()
     P.seq_len, P.num_v_heads = 1, 24  # 24 % 16 != 0
@@ -112,6 +112,12 @@ def test_decode_rejects_bad_layout_without_launch():
     P.new_state = fake + 4  # misaligned
     rc = lib.gdn_decode_launch(ctypes.byref(P), None)
     assert rc == _lib.GDN_ELAYOUT and "aligned" in _lib.last_error()
+    # seq_len > 1 reads the input state for every token: in place would race
+    P.new_state = P.state = fake
+    P.state_stride = P.new_state_stride
+    P.seq_len = 2
+    rc = lib.gdn_decode_launch(ctypes.byref(P), None)
+    assert rc == _lib.GDN_EINVAL and "alias" in _lib.last_error()
 
 
 def test_prefill_workspace_size_rejects_bad_sizes():

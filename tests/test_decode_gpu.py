@@ -175,3 +175,42 @@ def test_decode_matches_exact_fixture(dev):
                          float(f["scale"]))
     torch.cuda.synchronize()
     _check(out[0, 0], ns[0], f["out"][t], f["new_state"][1], "exact fixture")
+
+
+@pytest.mark.parametrize("batch,seq_len", [(3, 2), (5, 4), (64, 3)])
+def test_decode_multi_token(dev, batch, seq_len):
+    """seq_len > 1: every token is one step from the input state; new_state is the last
+    token's update (gdn_decode/solution/triton/kernel.py:110-118,146-147)."""
+    inp = decode_inputs(batch, seed=40 + seq_len, seq_len=seq_len)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out, ns = gdn_decode(*g.args())
+    torch.cuda.synchronize()
+    assert out.shape == (batch, seq_len, 32, 128)
+    _check(out, ns, ref_out, ref_ns, f"B={batch} T={seq_len}")
+    # the last token alone gives the same bits
+    last = decode_inputs(batch, seed=40 + seq_len, seq_len=seq_len)
+    for f in ("q", "k", "v", "a", "b"):
+        setattr(last, f, getattr(last, f)[:, -1:])
+    o1, s1 = gdn_decode(*last.to(dev).args())
+    torch.cuda.synchronize()
+    assert torch.equal(o1[:, 0], out[:, -1]) and torch.equal(s1, ns)
+
+
+def test_decode_multi_token_in_place_and_strided(dev):
+    """seq_len > 1 with new_state = state (the wrapper reads a copy) and token-strided
+    views of a wider q/k/v buffer."""
+    B, T, HQK, HV, D = 4, 3, 16, 32, 128
+    inp = decode_inputs(B, seed=77, seq_len=T)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    qkv = torch.zeros((B, T, 2 * HQK + HV, D), dtype=torch.bfloat16, device=dev)
+    qkv[:, :, :HQK] = g.q
+    qkv[:, :, HQK:2 * HQK] = g.k
+    qkv[:, :, 2 * HQK:] = g.v
+    q, k, v = qkv[:, :, :HQK], qkv[:, :, HQK:2 * HQK], qkv[:, :, 2 * HQK:]
+    out, ns = gdn_decode(q, k, v, g.state, g.A_log, g.a, g.dt_bias, g.b, g.scale,
+                         new_state=g.state)
+    torch.cuda.synchronize()
+    assert ns.data_ptr() == g.state.data_ptr()
+    _check(out, ns, ref_out, ref_ns, "T=3 in place, strided")
