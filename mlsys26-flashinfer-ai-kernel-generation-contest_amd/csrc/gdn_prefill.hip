@@ -623,10 +623,15 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     // records exist only for chunk ids < header[0] (see the plan kernel's clamp)
     const int nck = min((len + kC - 1) / kC, max(p.header[0] - c0, 0));
 
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
+    // w is wave-uniform: LDS copy destinations (M0) are then scalar arithmetic
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
+              lr = l & 15, lg = l >> 4;
     const int v0w = v0 + 16 * w;
 
-    // ---- copy plan (per lane; chunk-invariant parts)
+    // ---- copy plan. Every copy is a buffer load straight to LDS; per-lane source offsets
+    // are chunk-invariant and computed once. Rows past a chunk's end fall outside the
+    // chunk's buffer range and read as zero: those rows meet beta = 0 or the causal mask
+    // only, and their outputs are never stored.
     const uint32_t kst2 = (uint32_t)p.k_st * 2, qst2 = (uint32_t)p.q_st * 2;
     const uint32_t vst2 = (uint32_t)p.v_st * 2, ost2 = (uint32_t)p.o_st * 2;
     const char *kbase = (const char *)(p.k + (int64_t)tok0 * p.k_st + g * p.k_sh);
@@ -642,49 +647,81 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     constexpr int NWIN = 32 + VWIN + 19;       // all windows
     constexpr int PER = (NWIN + NW - 1) / NW;  // windows per wave
 
-    // Window i (compile-time) of this wave's share of chunk c.
-    auto issue_win = [&](ScanBuf<NW> &B, int c, const int i) {
+    // Source offset of this lane in window i (compile-time) of this wave; window kinds
+    // follow win = w + NW i: K rows 4b..4b+3 (16 windows), Q (16), V (NW == 8: 4 rows per
+    // window, NW == 4: 8 rows), then 18 T' / P' block pairs and the gate area.
+    uint32_t woff[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int win = w + NW * i;
+        uint32_t off = 0;
+        if (NW * i < 16) {
+            const int t = 4 * win + (l >> 4), cs = l & 15;
+            off = (uint32_t)t * kst2 + 16u * (cs ^ kswz(t));
+        } else if (NW * i < 32) {
+            const int t = 4 * (win - 16) + (l >> 4), cs = l & 15;
+            off = (uint32_t)t * qst2 + 16u * (cs ^ (t & 15));
+        } else if (NW * i < 32 + VWIN) {
+            const int b = win - 32;
+            const int t = NW == 8 ? 4 * b + (l >> 4) : 8 * b + (l >> 3);
+            const int cs = NW == 8 ? (l & 15) : (l & 7);
+            off = (uint32_t)t * vst2 + 16u * (cs ^ (2 * (t & 3)));
+        } else {
+            const int r = win - 32 - VWIN;
+            if (r < 18) {
+                const int mt = r / 6, pr = r % 6, d0 = pr < 3 ? 4 * pr : 2 * pr + 4;
+                const int d = d0 + (l >> 5), bi = d >> 2, bj = d & 3;
+                const int u = (l & 31) ^ (8 * (bi & 1)), rho = u >> 1, hf = (u & 1) ^ (rho >> 3);
+                const int mbase = mt == 0 ? kRecThi : (mt == 1 ? kRecTlo : kRecP);
+                off = bj <= bi ? (uint32_t)(mbase + (tri_blk(bi, bj) * 32 + 2 * rho + hf) * 16)
+                               : (uint32_t)kRecZero;
+            } else {
+                off = kRecGates + 16u * l;
+            }
+        }
+        woff[i] = off;
+    }
+
+    // Buffer ranges of chunk c: K / Q / V end after the chunk's last row.
+    struct ChunkSrc {
+        __amdgpu_buffer_rsrc_t k, q, v, r;
+    };
+    auto chunk_src = [&](int c) {
         const int lenc = min(kC, len - c * kC);
-        const char *kc_ = kbase + c * kstep, *qc_ = qbase + c * qstep, *vc_ = vbase + c * vstep;
-        const char *rc_ = rbase + c * rstep;
-        {
-            const int win = w + NW * i;  // window kind is a compile-time function of i
-            if (NW * i < 16) {
-                const int t = 4 * win + (l >> 4), cs = l & 15;
-                const uint32_t off = (uint32_t)min(t, lenc - 1) * kst2 + 16u * (cs ^ kswz(t));
-                dma16(kc_ + off, &B.K[64 * win]);
-            } else if (NW * i < 32) {
-                const int b = win - 16, t = 4 * b + (l >> 4), cs = l & 15;
-                const uint32_t off = (uint32_t)min(t, lenc - 1) * qst2 + 16u * (cs ^ (t & 15));
-                dma16(qc_ + off, &B.Q[64 * b]);
-            } else if (NW * i < 32 + VWIN) {
-                const int b = win - 32;
-                const int t = NW == 8 ? 4 * b + (l >> 4) : 8 * b + (l >> 3);
-                const int cs = NW == 8 ? (l & 15) : (l & 7);
-                const uint32_t off = (uint32_t)min(t, lenc - 1) * vst2 + 16u * (cs ^ (2 * (t & 3)));
-                dma16(vc_ + off, &B.V[64 * b]);
-            } else if (win < NWIN) {
-                const int r = win - 32 - VWIN;
-                if (r < 18) {
-                    const int mt = r / 6, pr = r % 6, d0 = pr < 3 ? 4 * pr : 2 * pr + 4;
-                    const int d = d0 + (l >> 5), bi = d >> 2, bj = d & 3;
-                    const int u = (l & 31) ^ (8 * (bi & 1)), rho = u >> 1, hf = (u & 1) ^ (rho >> 3);
-                    const int mbase = mt == 0 ? kRecThi : (mt == 1 ? kRecTlo : kRecP);
-                    const uint32_t off = bj <= bi
-                        ? (uint32_t)(mbase + (tri_blk(bi, bj) * 32 + 2 * rho + hf) * 16)
-                        : (uint32_t)kRecZero;
-                    u32x4 *dst = mt == 2 ? &B.P[32 * d0] : &B.T[mt][32 * d0];
-                    dma16(rc_ + off, dst);
-                } else {
-                    dma16(rc_ + kRecGates + 16 * l, &B.G[0]);
-                }
+        ChunkSrc cs;
+        cs.k = __builtin_amdgcn_make_buffer_rsrc((void *)(kbase + c * kstep), 0,
+                                                 (int)((uint32_t)(lenc - 1) * kst2 + 256u), 0x00020000);
+        cs.q = __builtin_amdgcn_make_buffer_rsrc((void *)(qbase + c * qstep), 0,
+                                                 (int)((uint32_t)(lenc - 1) * qst2 + 256u), 0x00020000);
+        cs.v = __builtin_amdgcn_make_buffer_rsrc((void *)(vbase + c * vstep), 0,
+                                                 (int)((uint32_t)(lenc - 1) * vst2 + 32u * NW), 0x00020000);
+        cs.r = __builtin_amdgcn_make_buffer_rsrc((void *)(rbase + c * rstep), 0, kRecBytes, 0x00020000);
+        return cs;
+    };
+    auto issue_win = [&](ScanBuf<NW> &B, const ChunkSrc &cs, const int i) {
+        const int win = w + NW * i;  // window kind is a compile-time function of i
+        if (NW * i < 16) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.k, (GDN_LDS void *)&B.K[64 * win], 16, woff[i], 0, 0, 0);
+        } else if (NW * i < 32) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.q, (GDN_LDS void *)&B.Q[64 * (win - 16)], 16, woff[i], 0, 0, 0);
+        } else if (NW * i < 32 + VWIN) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.v, (GDN_LDS void *)&B.V[64 * (win - 32)], 16, woff[i], 0, 0, 0);
+        } else if (win < NWIN) {
+            const int r = win - 32 - VWIN;
+            if (r < 18) {
+                const int mt = r / 6, pr = r % 6, d0 = pr < 3 ? 4 * pr : 2 * pr + 4;
+                u32x4 *dst = mt == 2 ? &B.P[32 * d0] : &B.T[mt][32 * d0];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.r, (GDN_LDS void *)dst, 16, woff[i], 0, 0, 0);
+            } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.r, (GDN_LDS void *)&B.G[0], 16, woff[i], 0, 0, 0);
             }
         }
     };
     auto issue_chunk = [&](ScanBuf<NW> &B, int c) {
+        const ChunkSrc cs = chunk_src(c);
 #pragma unroll
         for (int i = 0; i < PER; ++i)
-            issue_win(B, c, i);
+            issue_win(B, cs, i);
     };
 
     // ---- LDS read offsets (bytes within a ScanBuf member; chunk-invariant)
@@ -726,11 +763,12 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     // all at once they queue behind each other and stall the issuing waves.
     auto compute = [&](ScanBuf<NW> &B, int c, ScanBuf<NW> &Bn, bool more) {
         const int lenc = min(kC, len - c * kC);
+        const ChunkSrc ncs = chunk_src(more ? c + 1 : c);
         auto dma_at = [&](const int slot) {  // slots 0..7: after (a) steps 0..3, (c) tiles 0..3
 #pragma unroll
             for (int i = 0; i < PER; ++i)
                 if ((i * 8) / PER == slot && more)
-                    issue_win(Bn, c + 1, i);
+                    issue_win(Bn, ncs, i);
         };
         const char *Kb = (const char *)B.K, *Qb = (const char *)B.Q, *Vb = (const char *)B.V;
         const char *Th = (const char *)B.T[0], *Tl = (const char *)B.T[1];
