@@ -566,13 +566,56 @@ struct ScanArgs {
     int HQK, HV, ratio, ngroups;
 };
 
-// Bank swizzles (16-byte units; every operand read below covers 16 distinct bank groups):
+// LDS layouts (16-byte units). A ds_read_b128 is served in four cycles of 16 lanes: the
+// lanes of one 32-lane half whose lane bits 2, 3, 4 have equal parity; a cycle is
+// conflict-free when its 16 lanes touch 16 distinct units modulo 256 bytes (measured on
+// gfx950). Every b128 operand read below meets that:
 //   K row t, k-chunk c (k = 8c .. 8c+7)   -> unit 16 t + (c ^ kswz(t))
 //   Q row t, k-chunk c                    -> unit 16 t + (c ^ (t & 15))
 //   V row t, v-chunk c                    -> unit 2 NW t + (c ^ 2 (t & 3))
-//   T' / P' block (i, j), row r, half h    -> unit 32 (4 i + j) + (bswz(r, h) ^ 8 (i & 1))
-__device__ __forceinline__ int kswz(int t) { return ((t & 3) << 2) | ((t >> 3) & 3); }
-__device__ __forceinline__ int bswz(int r, int h) { return 2 * r + (h ^ (r >> 3)); }
+//   T' row r, column chunk c (8 columns)  -> unit tlay(r, c)
+//   P' row r, column chunk c              -> unit play(r, c)
+// T' is read with rows in the permuted order of the X / U tiles, P' in token order; both
+// layouts are bit permutations of (r, c) that put a read's four free lane bits into the
+// low unit bits and its tile / k-step into high ones (additive offsets).
+__host__ __device__ constexpr int kswz(int t)
+{
+    return ((t & 1) ? 1 : 0) ^ ((t & 2) ? 14 : 0) ^ ((t & 8) ? 6 : 0) ^ ((t & 16) ? 4 : 0);
+}
+__host__ __device__ constexpr int tlay(int r, int c)
+{
+    return (r & 3) | (((r >> 3) & 1) << 2) | ((c & 1) << 3) | (((r >> 4) & 1) << 4) |
+           (((c >> 1) & 1) << 5) | ((c >> 2) << 6) | (((r >> 2) & 1) << 7) | ((r >> 5) << 8);
+}
+__host__ __device__ constexpr int play(int r, int c)
+{
+    return (r & 7) | ((c & 1) << 3) | (((r >> 3) & 1) << 4) | (((c >> 1) & 1) << 5) |
+           ((c >> 2) << 6) | (((r >> 4) & 1) << 7) | ((r >> 5) << 8);
+}
+// Inverses (unit -> row, column chunk), used by the record copies.
+__host__ __device__ constexpr int tlay_row(int u)
+{
+    return (u & 3) | (((u >> 7) & 1) << 2) | (((u >> 2) & 1) << 3) | (((u >> 4) & 1) << 4) |
+           ((u >> 8) << 5);
+}
+__host__ __device__ constexpr int play_row(int u)
+{
+    return (u & 7) | (((u >> 4) & 1) << 3) | (((u >> 7) & 1) << 4) | ((u >> 8) << 5);
+}
+__host__ __device__ constexpr int lay_col(int u)
+{
+    return ((u >> 3) & 1) | (((u >> 5) & 1) << 1) | (((u >> 6) & 1) << 2);
+}
+constexpr bool layouts_invert()
+{
+    for (int r = 0; r < 64; ++r)
+        for (int c = 0; c < 8; ++c)
+            if (tlay_row(tlay(r, c)) != r || lay_col(tlay(r, c)) != c ||
+                play_row(play(r, c)) != r || lay_col(play(r, c)) != c)
+                return false;
+    return true;
+}
+static_assert(layouts_invert(), "T' / P' LDS layouts must be bijections");
 
 // One chunk in LDS, as the workgroup's waves read it.
 template <int NW>
@@ -580,16 +623,17 @@ struct ScanBuf {
     u32x4 K[kC * 16];      // 16 KB
     u32x4 Q[kC * 16];      // 16 KB
     u32x4 V[kC * 2 * NW];  // the workgroup's 16 NW value columns
-    u32x4 T[2][16 * 32];   // T' hi / lo as 4 x 4 dense 16x16 blocks
-    u32x4 P[16 * 32];      // P' blocks
+    u32x4 T[2][512];       // T' hi / lo (tlay)
+    u32x4 P[512];          // P' (play)
     f32x4 G[64];           // the record's gate area (gamma, dec, scale gamma, gammaC)
 };
 
 // Copy windows of one chunk, 64 units (1 KB) each: K rows 4b..4b+3 (16 windows), Q (16),
-// V (NW == 8: 4 rows per window, NW == 4: 8 rows), then 18 T' / P' block pairs and the
-// gate area. Record windows read block pairs {(i, j), (i, j + 1)} of the dense layout
-// starting at blocks 0, 4, 8, 10, 12, 14; blocks above the diagonal read the record's
-// zero bytes.
+// V (NW == 8: 4 rows per window, NW == 4: 8 rows), then 6 windows each of T' hi, T' lo
+// and P' and the gate area. Each record window fills LDS units 64 b .. 64 b + 63 of its
+// matrix (b = 0, 2, 4, 5, 6, 7; windows 1 and 3 hold rows 0..31 x columns 32..63, which
+// no read touches) by gathering from the record's 16x16 blocks; units above the
+// diagonal read the record's zero bytes.
 
 // Workgroup: NW waves, each owning 16 state rows v0 + 16 w .. of one (sequence, v-head)
 // for all 128 columns; the waves share the chunk's K, Q, V, T', P' through LDS and
@@ -649,7 +693,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
 
     // Source offset of this lane in window i (compile-time) of this wave; window kinds
     // follow win = w + NW i: K rows 4b..4b+3 (16 windows), Q (16), V (NW == 8: 4 rows per
-    // window, NW == 4: 8 rows), then 18 T' / P' block pairs and the gate area.
+    // window, NW == 4: 8 rows), then 18 T' / P' windows and the gate area.
     uint32_t woff[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -669,11 +713,12 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         } else {
             const int r = win - 32 - VWIN;
             if (r < 18) {
-                const int mt = r / 6, pr = r % 6, d0 = pr < 3 ? 4 * pr : 2 * pr + 4;
-                const int d = d0 + (l >> 5), bi = d >> 2, bj = d & 3;
-                const int u = (l & 31) ^ (8 * (bi & 1)), rho = u >> 1, hf = (u & 1) ^ (rho >> 3);
+                const int mt = r / 6, pr = r % 6, b = pr == 0 ? 0 : (pr == 1 ? 2 : pr + 2);
+                const int u = 64 * b + l;  // this lane's LDS unit
+                const int row = mt < 2 ? tlay_row(u) : play_row(u), cc = lay_col(u);
+                const int bi = row >> 4, bj = cc >> 1;
                 const int mbase = mt == 0 ? kRecThi : (mt == 1 ? kRecTlo : kRecP);
-                off = bj <= bi ? (uint32_t)(mbase + (tri_blk(bi, bj) * 32 + 2 * rho + hf) * 16)
+                off = bj <= bi ? (uint32_t)(mbase + (tri_blk(bi, bj) * 32 + 2 * (row & 15) + (cc & 1)) * 16)
                                : (uint32_t)kRecZero;
             } else {
                 off = kRecGates + 16u * l;
@@ -709,8 +754,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         } else if (win < NWIN) {
             const int r = win - 32 - VWIN;
             if (r < 18) {
-                const int mt = r / 6, pr = r % 6, d0 = pr < 3 ? 4 * pr : 2 * pr + 4;
-                u32x4 *dst = mt == 2 ? &B.P[32 * d0] : &B.T[mt][32 * d0];
+                const int mt = r / 6, pr = r % 6, b = pr == 0 ? 0 : (pr == 1 ? 2 : pr + 2);
+                u32x4 *dst = mt == 2 ? &B.P[64 * b] : &B.T[mt][64 * b];
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.r, (GDN_LDS void *)dst, 16, woff[i], 0, 0, 0);
             } else {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.r, (GDN_LDS void *)&B.G[0], 16, woff[i], 0, 0, 0);
@@ -727,20 +772,16 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     // ---- LDS read offsets (bytes within a ScanBuf member; chunk-invariant)
     const int c_ = lr & 3, r_ = lr >> 2;
     uint32_t koffA[4], ktoff[4], qoff[4];
+    const int ta = 8 * (lr >> 2) + (lr & 3), tk = 8 * lg + r_;  // rows of the K and K^T reads
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        koffA[s] = 16u * (16 * (8 * (lr >> 2) + (lr & 3)) + (((s ^ (lr & 3)) << 2) | (lg ^ (lr >> 2))));
-        ktoff[s] = 256u * (8 * lg + r_) + 16u * (((s ^ r_) << 2) | (c_ ^ lg));
+        koffA[s] = 16u * (16 * ta + ((4 * s + lg) ^ kswz(ta)));
+        ktoff[s] = 256u * tk + 16u * ((4 * s + c_) ^ kswz(tk));
         qoff[s] = 16u * (16 * lr + ((4 * s + lg) ^ lr));
     }
     const uint32_t voff = 32u * NW * (8 * lg + r_) + 16u * ((2 * w + (c_ >> 1)) ^ (2 * r_)) + 8u * (c_ & 1);
-    const int mu = lr >> 3, a_ = (lr >> 2) & 1, lam = lg >> 1, hf = lg & 1;
-    uint32_t toff[2], poff[2];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        toff[b] = 512u * (4 * mu + lam) + 16u * ((16 * a_ + 8 * b + 2 * (lr & 3) + (hf ^ a_)) ^ (8 * mu));
-        poff[b] = 512u * lam + 16u * (bswz(lr, hf) ^ (8 * b));
-    }
+    // T' / P' operand of tile tt, k-step sp: byte tpoff + 2048 tt + 1024 sp
+    const uint32_t tpoff = 16u * (lr & 7) + 128u * (lg & 1) + 256u * (lr >> 3) + 512u * (lg >> 1);
     const uint32_t goff = 32u * lg, sgoff = 4u * lr;
 
     // ---- state: S[2 s + h] holds S[v0w + lr][32 s + 8 lg + 4 h + i], i = 0..3
@@ -825,7 +866,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         // (b) R = V - gamma X -> operands (hi + lo) over token blocks s'
         u32x4 Rh[2], Rl[2];
         auto tRead = [&](int tt, int sp, u32x4 &th, u32x4 &tl) {
-            const uint32_t o = toff[tt & 1] + 512 * (8 * (tt >> 1) + 2 * sp);
+            const uint32_t o = tpoff + 2048 * tt + 1024 * sp;
             th = *(const u32x4 *)(Th + o);
             tl = *(const u32x4 *)(Tl + o);
         };
@@ -879,7 +920,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 qv[s2] = *(const u32x4 *)(Qb + qoff[s2] + 4096 * tt);
 #pragma unroll
             for (int sp = 0; sp <= (tt >> 1); ++sp)
-                pv[sp] = *(const u32x4 *)(Pb + poff[tt & 1] + 512 * (4 * tt + 2 * sp));
+                pv[sp] = *(const u32x4 *)(Pb + tpoff + 2048 * tt + 1024 * sp);
         };
         u32x4 qA[2][4], pA[2][2];
         qRead(0, qA[0], pA[0]);
@@ -910,6 +951,17 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
             }
         };
         u32x4 kt[2][2];
+        // Tile tt's combine and store run after tile tt + 1's MFMAs are issued, so they
+        // never wait on the MFMA chain that produced them.
+        f32x4 Oi[2], Oa[2];
+        float sg[2];
+        auto out_epi = [&](int tt) {
+            const int cb = tt & 1;
+            const uint32_t o01 = pack_bf16x2(fmaf(sg[cb], Oi[cb][0], Oa[cb][0]), fmaf(sg[cb], Oi[cb][1], Oa[cb][1]));
+            const uint32_t o23 = pack_bf16x2(fmaf(sg[cb], Oi[cb][2], Oa[cb][2]), fmaf(sg[cb], Oi[cb][3], Oa[cb][3]));
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{o01, o23}, orsrc,
+                                                  (int)((uint32_t)(16 * tt + lr) * ost2 + 8u * lg), 0, 0);
+        };
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
             __builtin_amdgcn_sched_barrier(0);
@@ -918,18 +970,17 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 qRead(tt + 1, qA[cb ^ 1], pA[cb ^ 1]);
             else
                 ktRead(0, kt[0]);  // (f)'s first operands
-            f32x4 Oi = {0.f, 0.f, 0.f, 0.f}, Oa = {0.f, 0.f, 0.f, 0.f};
+            sg[cb] = *(const float *)(Gb + 512 + sgoff + 64 * tt);
+            Oi[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            Oa[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2)
-                Oi = mfma_bf16(Bh[s2], qA[cb][s2], Oi);
+                Oi[cb] = mfma_bf16(Bh[s2], qA[cb][s2], Oi[cb]);
 #pragma unroll
             for (int sp = 0; sp <= (tt >> 1); ++sp)
-                Oa = mfma_bf16(Ub[sp], pA[cb][sp], Oa);
-            const float sg = *(const float *)(Gb + 512 + sgoff + 64 * tt);
-            const uint32_t o01 = pack_bf16x2(fmaf(sg, Oi[0], Oa[0]), fmaf(sg, Oi[1], Oa[1]));
-            const uint32_t o23 = pack_bf16x2(fmaf(sg, Oi[2], Oa[2]), fmaf(sg, Oi[3], Oa[3]));
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{o01, o23}, orsrc,
-                                                  (int)((uint32_t)(16 * tt + lr) * ost2 + 8u * lg), 0, 0);
+                Oa[cb] = mfma_bf16(Ub[sp], pA[cb][sp], Oa[cb]);
+            if (tt > 0)
+                out_epi(tt - 1);
         }
 
         // (f) S = gammaC S0 + W^T K
@@ -945,6 +996,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 acc = mfma_bf16(kt[gidx & 1][sp], Wh[sp], acc);
                 acc = mfma_bf16(kt[gidx & 1][sp], Wl[sp], acc);
             }
+            if (gidx == 0)
+                out_epi(3);
             S[gidx] = acc;
         }
         __builtin_amdgcn_sched_barrier(0);
