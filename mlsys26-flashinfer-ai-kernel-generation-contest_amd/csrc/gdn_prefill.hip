@@ -210,7 +210,8 @@ __device__ __forceinline__ void dma_barrier()
 struct PrepArgs {
     const bf16_t *q, *k, *a, *b;
     const float *A_log, *dt_bias;
-    int64_t q_st, q_sh, k_st, k_sh, a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
+    // element strides, host-checked to fit 31 bits (32-bit here keeps scalar registers free)
+    int32_t q_st, q_sh, k_st, k_sh, a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
     const int32_t *header, *chunk_tok0, *chunk_len;
     char *records;
     int HQK, HV, ratio;
@@ -244,7 +245,8 @@ __device__ __forceinline__ int pi16(int m) { return 4 * (m & 3) + (m >> 2); }
 //   * after a barrier (all X_i and A blocks published): column block w of T = (I + A)^-1,
 //       T_ww = X_w,  T_iw = -X_i sum_{m=w}^{i-1} A_im T_mw  (i > w),
 //     on fp32 MFMA with every operand in registers, and writes T' = T diag(beta);
-// wave (hv, 0) also computes the next unit's gates and cumulative log2 decay L.
+// wave (hv, 3), which has the least work after the barrier, also computes the next unit's
+// gates and cumulative log2 decay L.
 // (gdn_prefill/solution/triton/kernel.py:60-79 form the same A, T and P.)
 template <int VH>
 struct PrepSmem {
@@ -258,12 +260,16 @@ struct PrepSmem {
     float Ms[4 * VH][16][16];  // per wave: -A_ww rows, X_w, then T' staging
 };
 
+constexpr int kGateWave = 3;  // column block with no work after the barrier
+
 template <int VH>
 __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 {
     const int ngrp = p.ratio / VH;
     const int nunits = p.header[0] * p.HQK * ngrp;
-    const int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
+    // wv is wave-uniform: branches on the column block are scalar branches
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
+              lr = l & 15, lg = l >> 4;
     // Waves are dealt to the 4 SIMDs round-robin: the second v-head takes the blocks in
     // reverse, so each SIMD pairs a heavy column block (w = 0) with a light one.
     const int hv = wv >> 2, w = hv & 1 ? 3 - (wv & 3) : (wv & 3);
@@ -286,8 +292,8 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     // dealt to the waves. Rows past the chunk's end repeat its last token: they meet
     // beta = 0 or the causal mask only.
     auto copy = [&](const Unit &U, bool isq, u32x4 *dst) {
-        const char *base = isq ? (const char *)(p.q + (int64_t)U.tok0 * p.q_st + U.g * p.q_sh)
-                               : (const char *)(p.k + (int64_t)U.tok0 * p.k_st + U.g * p.k_sh);
+        const char *base = isq ? (const char *)(p.q + (int64_t)U.tok0 * p.q_st + (int64_t)U.g * p.q_sh)
+                               : (const char *)(p.k + (int64_t)U.tok0 * p.k_st + (int64_t)U.g * p.k_sh);
         const uint32_t st2 = isq ? qst2 : kst2;
 #pragma unroll
         for (int i = 0; i < 4 / VH; ++i) {
@@ -301,15 +307,15 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow).
     auto gate_in = [&](const Unit &U, float &a_in, float &b_in) {
         const int tl = U.tok0 + min(l, U.len - 1);
-        a_in = bf16_to_f32(p.a[(int64_t)tl * p.a_st + U.h * p.a_sh]);
-        b_in = bf16_to_f32(p.b[(int64_t)tl * p.b_st + U.h * p.b_sh]);
+        a_in = bf16_to_f32(p.a[(int64_t)tl * p.a_st + (int64_t)U.h * p.a_sh]);
+        b_in = bf16_to_f32(p.b[(int64_t)tl * p.b_st + (int64_t)U.h * p.b_sh]);
     };
     auto gates = [&](const Unit &U, float a_in, float b_in, int buf) {
         float la = 0.f, bt = 0.f;
         if (l < U.len) {
-            const float x = a_in + p.dt_bias[U.h * p.dt_s];
+            const float x = a_in + p.dt_bias[(int64_t)U.h * p.dt_s];
             const float sp = x > 20.f ? x : logf(1.f + expf(x));
-            la = -expf(p.A_log[U.h * p.A_log_s]) * sp;
+            la = -expf(p.A_log[(int64_t)U.h * p.A_log_s]) * sp;
             bt = 1.f / (1.f + expf(-b_in));
         }
         float L = la * 1.44269504088896340736f;
@@ -346,7 +352,8 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
         const float *Ls = sm.L[buf][hv], *Bs = sm.B[buf][hv], *LsT = sm.LT[buf][hv];
 
-        // P' row block w: lane (t = 16 w + lr, lg) holds columns 16 jb + 4 lg .. +3.
+        // P' row block w: lane (t = 16 w + lr, lg) holds columns 16 jb + 4 lg .. +3. All
+        // blocks' MFMAs issue before any scaling / store, which then never waits on them.
         {
             const int t = 16 * w + lr;
             const float Lt = Ls[t];
@@ -354,20 +361,26 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
                 qn[ks] = kop(sm.Q, t, ks);
+            f32x4 rp[4];
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
                 if (jb > w)
                     break;
-                f32x4 r = {0.f, 0.f, 0.f, 0.f};
+                rp[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
-                    r = mfma_bf16(kop(Kb, 16 * jb + lr, ks), qn[ks], r);
+                    rp[jb] = mfma_bf16(kop(Kb, 16 * jb + lr, ks), qn[ks], rp[jb]);
+            }
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                if (jb > w)
+                    break;
                 const f32x4 Lj = *(const f32x4 *)&Ls[16 * jb + 4 * lg];
                 float pv[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = 16 * jb + 4 * lg + e;
-                    const float v = p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * r[e];
+                    const float v = p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * rp[jb][e];
                     pv[e] = (jb < w || j <= t) ? v : 0.f;  // only the diagonal block is masked
                 }
                 *(u32x2 *)(rec + kRecP + 2 * (tri_blk(w, jb) * kBlk + lr * 16 + 4 * lg)) =
@@ -375,33 +388,44 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
             }
         }
 
-        // A column block w: lane (lr, lg) element e = A[16 i + pi(lr)][16 w + 4 e + lg].
+        // A column block w: lane (lr, lg) element e = A[16 i + pi(lr)][16 w + 4 e + lg],
+        // blocks i = w .. 3; MFMAs first, then scaling.
         f32x4 Aww = {0.f, 0.f, 0.f, 0.f};
+        {
+            u32x4 kw[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int ks = 0; ks < 4; ++ks)
+                kw[ks] = kop(Kb, 16 * w + pi16(lr), ks);
+            f32x4 ra[4];
 #pragma unroll
-            for (int m = 0; m <= i; ++m) {  // only m == w runs; unrolled so blocks index statically
-                if (m != w)
-                    continue;
-                f32x4 r = {0.f, 0.f, 0.f, 0.f};
+            for (int i = 3; i >= 0; --i) {
+                if (i < w)
+                    break;
+                ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
-                    r = mfma_bf16(kop(Kb, 16 * m + pi16(lr), ks), kop(Kb, 16 * i + pi16(lr), ks), r);
+                    ra[i] = mfma_bf16(kw[ks], kop(Kb, 16 * i + pi16(lr), ks), ra[i]);
+            }
+            const f32x4 Lm = *(const f32x4 *)&LsT[16 * w + 4 * lg];
+#pragma unroll
+            for (int i = 3; i >= 0; --i) {
+                if (i < w)
+                    break;
                 const int t = 16 * i + pi16(lr);
                 const float Lt = Ls[t], btt = Bs[t];
-                const f32x4 Lm = *(const f32x4 *)&LsT[16 * m + 4 * lg];
                 f32x4 av;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int j = 16 * m + 4 * e + lg;
-                    const float v = btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * r[e];
-                    av[e] = (m < i || j < t) ? v : 0.f;  // only the diagonal block is masked
+                    const int j = 16 * w + 4 * e + lg;
+                    const float v = btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * ra[i][e];
+                    av[e] = (w < i || j < t) ? v : 0.f;  // only the diagonal block is masked
                 }
-                if (i == m)
+                if (i == w)
                     Aww = av;
                 else
-                    sm.AO[hv][i * (i - 1) / 2 + m][l] = av;
+                    sm.AO[hv][i * (i - 1) / 2 + w][l] = av;
             }
+        }
 
         // X_w = (I + A_ww)^-1. Lane (lr, lg) holds row pi(lr), columns lg + 4 s (s = 0..3)
         // of X; step m subtracts A[r][m] x (row m of X), row m being final (A is strictly
@@ -490,7 +514,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         }
 
         // next unit's gates (its inputs were loaded one unit ago)
-        if (more && w == 0)
+        if (more && w == kGateWave)
             gates(N, na, nb, buf ^ 1);
     };
 
@@ -501,7 +525,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     float a_in = 0.f, b_in = 0.f;
     copy(U, false, sm.K[0]);
     copy(U, true, sm.Q);
-    if (w == 0) {
+    if (w == kGateWave) {
         gate_in(U, a_in, b_in);
         gates(U, a_in, b_in, 0);
     }
@@ -513,7 +537,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         dma_barrier();
         if (more) {
             copy(N, false, sm.K[1]);
-            if (w == 0)
+            if (w == kGateWave)
                 gate_in(N, a_in, b_in);
         }
         compute(U, sm.K[0], 0, a_in, b_in, N, more);
@@ -528,7 +552,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         dma_barrier();
         if (more) {
             copy(N, false, sm.K[0]);
-            if (w == 0)
+            if (w == kGateWave)
                 gate_in(N, a_in, b_in);
         }
         compute(U, sm.K[1], 1, a_in, b_in, N, more);
@@ -1152,6 +1176,14 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
             p->output_stride[i] < 0)
             return gdn_set_error(GDN_ELAYOUT,
                                  "gdn_prefill: token / head strides must be in [0, 2^24)");
+    const int64_t kMaxGateStride = int64_t(1) << 31;
+    for (int i = 0; i < 2; ++i)
+        if (p->a_stride[i] < 0 || p->a_stride[i] >= kMaxGateStride || p->b_stride[i] < 0 ||
+            p->b_stride[i] >= kMaxGateStride)
+            return gdn_set_error(GDN_ELAYOUT, "gdn_prefill: a / b strides must be in [0, 2^31)");
+    if (p->A_log_stride < 0 || p->A_log_stride >= kMaxGateStride || p->dt_bias_stride < 0 ||
+        p->dt_bias_stride >= kMaxGateStride)
+        return gdn_set_error(GDN_ELAYOUT, "gdn_prefill: A_log / dt_bias strides must be in [0, 2^31)");
     const Layout L = layout(T, N, HV);
     if (L.nc > 0x7fffffff)
         return gdn_set_error(GDN_EINVAL, "gdn_prefill: too many chunks");
@@ -1202,16 +1234,16 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         qa.b = (const gdn::bf16_t *)p->b;
         qa.A_log = p->A_log;
         qa.dt_bias = p->dt_bias;
-        qa.q_st = p->q_stride[0];
-        qa.q_sh = p->q_stride[1];
-        qa.k_st = p->k_stride[0];
-        qa.k_sh = p->k_stride[1];
-        qa.a_st = p->a_stride[0];
-        qa.a_sh = p->a_stride[1];
-        qa.b_st = p->b_stride[0];
-        qa.b_sh = p->b_stride[1];
-        qa.A_log_s = p->A_log_stride;
-        qa.dt_s = p->dt_bias_stride;
+        qa.q_st = (int32_t)p->q_stride[0];
+        qa.q_sh = (int32_t)p->q_stride[1];
+        qa.k_st = (int32_t)p->k_stride[0];
+        qa.k_sh = (int32_t)p->k_stride[1];
+        qa.a_st = (int32_t)p->a_stride[0];
+        qa.a_sh = (int32_t)p->a_stride[1];
+        qa.b_st = (int32_t)p->b_stride[0];
+        qa.b_sh = (int32_t)p->b_stride[1];
+        qa.A_log_s = (int32_t)p->A_log_stride;
+        qa.dt_s = (int32_t)p->dt_bias_stride;
         qa.header = pa.header;
         qa.chunk_tok0 = pa.chunk_tok0;
         qa.chunk_len = pa.chunk_len;
