@@ -192,3 +192,22 @@ def test_prefill_matches_exact_fixture(dev):
                           torch.from_numpy(f["cu_seqlens"]).to(dev), float(f["scale"]))
     torch.cuda.synchronize()
     _check(out, ns, f["out"], f["new_state"], "exact fixture")
+
+
+@pytest.mark.parametrize("nseq", [255, 300, 600])
+def test_prefill_many_sequences(dev, nseq):
+    """Hundreds of short and empty sequences: the planning kernel's chunk table and
+    longest-first order (its sort covers up to 512 sequences) drive prep and scan."""
+    g = torch.Generator().manual_seed(nseq)
+    lens = [int(x) for x in torch.randint(0, 90, (nseq,), generator=g)]
+    _run(dev, prefill_inputs(lens, hqk=4, hv=8, seed=nseq, with_state=True), f"N={nseq}")
+
+
+@pytest.mark.parametrize("nseq", [3, 300])
+def test_prefill_gap_before_first_sequence(dev, nseq):
+    """cu_seqlens[0] > 0: the leading tokens belong to no sequence and read as zero."""
+    g = torch.Generator().manual_seed(7 + nseq)
+    lens = [int(x) for x in torch.randint(1, 70, (nseq,), generator=g)]
+    inp = prefill_inputs(lens, hqk=4, hv=8, seed=31, with_state=True, pad_tokens=53)
+    inp.cu_seqlens = inp.cu_seqlens + 37  # 37 leading and 16 trailing gap tokens
+    _run(dev, inp, f"lead gap N={nseq}")
