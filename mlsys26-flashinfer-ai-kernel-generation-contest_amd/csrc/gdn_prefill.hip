@@ -68,6 +68,27 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// DPP move with a row / bank mask: disabled rows and out-of-row sources read 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_or0(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xF, true));
+}
+
+// Inclusive prefix sum over the 64 lanes: shifts by 1, 2, 4, 8 inside each 16-lane row,
+// then row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then the total of
+// rows 0-1 into rows 2-3 (row_bcast:31).
+__device__ __forceinline__ float wave_prefix_sum(float x)
+{
+    x += dpp_or0<0x111, 0xF>(x);
+    x += dpp_or0<0x112, 0xF>(x);
+    x += dpp_or0<0x114, 0xF>(x);
+    x += dpp_or0<0x118, 0xF>(x);
+    x += dpp_or0<0x142, 0xA>(x);
+    x += dpp_or0<0x143, 0xC>(x);
+    return x;
+}
+
 template <int K>
 __device__ __forceinline__ float quad_bcast(float x)
 {
@@ -311,21 +332,19 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         b_in = bf16_to_f32(p.b[(int64_t)tl * p.b_st + (int64_t)U.h * p.b_sh]);
     };
     auto gates = [&](const Unit &U, float a_in, float b_in, int buf) {
-        float la = 0.f, bt = 0.f;
+        // log2 alpha = -exp(A_log) log2(1 + e^x) (x > 20: -exp(A_log) x log2 e), with the
+        // hardware base-2 exp / log; beta = 1 / (1 + e^-b)
+        constexpr float kLog2e = 1.44269504088896340736f;
+        float L = 0.f, bt = 0.f;
         if (l < U.len) {
             const float x = a_in + p.dt_bias[(int64_t)U.h * p.dt_s];
-            const float sp = x > 20.f ? x : logf(1.f + expf(x));
-            la = -expf(p.A_log[(int64_t)U.h * p.A_log_s]) * sp;
-            bt = 1.f / (1.f + expf(-b_in));
+            const float sp2 = x > 20.f ? x * kLog2e
+                                       : __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(x * kLog2e));
+            L = -expf(p.A_log[(int64_t)U.h * p.A_log_s]) * sp2;
+            bt = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-b_in * kLog2e));
         }
-        float L = la * 1.44269504088896340736f;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(L, off, 64);
-            if (l >= off)
-                L += y;
-        }
-        const float Lend = __shfl(L, 63, 64);
+        L = wave_prefix_sum(L);  // cumulative log2 decay
+        const float Lend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 63));
         sm.L[buf][hv][l] = L;
         sm.B[buf][hv][l] = bt;
         sm.LT[buf][hv][16 * (l >> 4) + 4 * (l & 3) + ((l >> 2) & 3)] = L;
