@@ -120,7 +120,11 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
         // valid input sum(ceil(len / C)) <= ceil(T / C) + N = nc always holds.
         __shared__ int64_t scan[256];
         __shared__ int32_t s_nck[kPlanSortMax];
+        // up to kPlanSortMax sequences the chunk table is filled chunk-parallel from these
+        __shared__ int32_t s_first[kPlanSortMax], s_end[kPlanSortMax], s_t0[kPlanSortMax],
+            s_len[kPlanSortMax];
         __shared__ int64_t s_carry;
+        const bool par = p.N <= kPlanSortMax;
         if (tid == 0)
             s_carry = 0;
         __syncthreads();
@@ -150,9 +154,16 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
             const int64_t first = s_carry + scan[tid] - nck;
             if (n < p.N) {
                 p.seq_chunk0[n] = (int32_t)(first < p.nc ? first : p.nc);
-                for (int i = 0; i < nck && first + i < p.nc; ++i) {
-                    p.chunk_tok0[first + i] = t0 + i * kC;
-                    p.chunk_len[first + i] = min(kC, ln - i * kC);
+                if (par) {
+                    s_first[n] = (int32_t)(first < p.nc ? first : p.nc);
+                    s_end[n] = (int32_t)(first + nck < p.nc ? first + nck : p.nc);
+                    s_t0[n] = t0;
+                    s_len[n] = ln;
+                } else {
+                    for (int i = 0; i < nck && first + i < p.nc; ++i) {
+                        p.chunk_tok0[first + i] = t0 + i * kC;
+                        p.chunk_len[first + i] = min(kC, ln - i * kC);
+                    }
                 }
             }
             __syncthreads();
@@ -164,6 +175,23 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
             const int32_t total = (int32_t)(s_carry < p.nc ? s_carry : p.nc);
             p.seq_chunk0[p.N] = total;
             p.header[0] = total;
+        }
+        if (par) {  // chunk c belongs to the first sequence whose chunks end after c
+            __syncthreads();
+            const int total = (int)(s_carry < p.nc ? s_carry : p.nc);
+            for (int c = tid; c < total; c += 256) {
+                int lo = 0, hi = p.N - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (s_end[mid] > c)
+                        hi = mid;
+                    else
+                        lo = mid + 1;
+                }
+                const int i = c - s_first[lo];
+                p.chunk_tok0[c] = s_t0[lo] + i * kC;
+                p.chunk_len[c] = min(kC, s_len[lo] - i * kC);
+            }
         }
         // Longest-first order (identity when N is large).
         if (p.N <= kPlanSortMax) {
