@@ -100,6 +100,32 @@ __device__ __forceinline__ int64_t load_cu(const void *cu, int cu64, int i)
     return cu64 ? ((const int64_t *)cu)[i] : (int64_t)((const int32_t *)cu)[i];
 }
 
+// Segment jobs. When (sequence, v-head) pairs are too few to fill the GPU, a long sequence
+// is cut into G segments scanned in parallel. The state map of a segment is affine,
+// S_out = S_in M_s + R_s. Pass A scans segment 0 from the true initial state, giving
+// S_in(1), and every middle segment s = 1 .. G - 2 twice from known states: value rows from
+// zero give R_s, identity rows with V = 0 give M_s. Pass C rescans each segment s >= 1 for
+// its outputs; its workgroups first chain S_in(s) = S_in(1) M_1 + R_1 ... (s - 1 steps) on
+// their own state rows, and the last segment's scan ends in the final state, so the last
+// segment needs no state map.
+constexpr int kJobFirst = 0;   // from the initial state; outputs; final state -> new_state,
+                               // or (slot >= 0) -> S_in(1)
+constexpr int kJobZero = 1;    // value rows from a zero state, no outputs: final state = R_s
+constexpr int kJobIdent = 2;   // identity rows with V = 0, no outputs: final state = M_s,
+                               // stored as bf16 hi / lo units of M^T
+constexpr int kJobResume = 3;  // from S_in(1) and (steps) chain steps; outputs; final state
+                               // -> new_state for the last segment
+// Slots hold one 128 x 128 fp32 matrix per (slot, v-head), each in the order its reader
+// wants, so that every copy reads whole lines:
+// * S_in(1) and R_s: register image of the scan's state layout, 16-byte unit
+//   (8 (row / 16) + t) 64 + lane holds row 16 (row / 16) + lane % 16, columns
+//   32 (t / 2) + 8 (lane / 16) + 4 (t % 2) + 0..3;
+// * M_s: LDS image of M_s^T split into bf16 hi units (0 .. 2047) then lo units; unit
+//   16 j + (cu ^ kswz(j)) holds M_s[8 cu .. 8 cu + 7][j].
+constexpr int64_t kSlotFloats = 128 * 128;
+constexpr int kMtUnits = 2048;
+constexpr int kSegMinChunks = 4;            // shortest segment
+
 // ------------------------------------------------------------------------- plan
 struct PlanArgs {
     const void *cu;
@@ -107,6 +133,11 @@ struct PlanArgs {
     int32_t *header, *chunk_tok0, *chunk_len, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
     bf16_t *out;
     int64_t o_st, o_sh;
+    // segments (seg_G >= 3): at most seg_G segments per sequence; job entries of 8 ints
+    // {sequence, kind, first chunk, end chunk, slot, chain steps, last}, pass A from
+    // jobs[0], pass C from jobs[8 seg_capA]; counts in header[1], header[2]
+    int seg_G, seg_capA;
+    int32_t *jobs;
 };
 
 constexpr int kPlanSortMax = 512;
@@ -194,6 +225,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
             }
         }
         // Longest-first order (identity when N is large).
+        __shared__ int32_t s_order[kPlanSortMax];
         if (p.N <= kPlanSortMax) {
             for (int n = tid; n < p.N; n += 256) {
                 const int mine = s_nck[n];
@@ -203,10 +235,58 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                     rank += (o > mine) || (o == mine && m < n);
                 }
                 p.seq_order[rank] = n;
+                s_order[rank] = n;
             }
         } else {
             for (int n = tid; n < p.N; n += 256)
                 p.seq_order[n] = n;
+        }
+        if (p.seg_G >= 3 && par) {  // segment job tables (host only asks for small N)
+            __syncthreads();
+            if (tid == 0) {
+                auto put = [&](int idx, int n, int kind, int cb, int ce, int q, int steps, int last) {
+                    int32_t *e = p.jobs + 8 * idx;
+                    e[0] = n;
+                    e[1] = kind;
+                    e[2] = cb;
+                    e[3] = ce;
+                    e[4] = q;
+                    e[5] = steps;
+                    e[6] = last;
+                };
+                // pass A: every segment 0 first (longest sequences first), then the state
+                // maps; slots q .. q + G - 2 of a sequence hold S_in(1) and M_s, R_s of the
+                // middle segments s (slot q + s - 1)
+                int na = 0, nc3 = 0;
+                for (int pass = 0; pass < 2; ++pass) {
+                    int qs = 0;
+                    for (int i = 0; i < p.N; ++i) {
+                        const int n = s_order[i];
+                        const int ncks = s_end[n] - s_first[n];
+                        int G = min(p.seg_G, max(1, ncks / kSegMinChunks));
+                        const int Ls = (ncks + G - 1) / G;
+                        G = Ls > 0 ? (ncks + Ls - 1) / Ls : 1;
+                        if (G < 3)
+                            G = 1;  // two segments would run one after the other
+                        const int q = G > 1 ? qs : -1;
+                        qs += G - 1;
+                        if (pass == 0) {
+                            put(na++, n, kJobFirst, 0, G > 1 ? Ls : ncks, q, 0, 0);
+                            continue;
+                        }
+                        for (int sg = 1; sg < G; ++sg) {
+                            const int cb = sg * Ls, ce = min(cb + Ls, ncks);
+                            if (sg < G - 1) {
+                                put(na++, n, kJobZero, cb, ce, q + sg - 1, 0, 0);
+                                put(na++, n, kJobIdent, cb, ce, q + sg - 1, 0, 0);
+                            }
+                            put(p.seg_capA + nc3++, n, kJobResume, cb, ce, q, sg - 1, sg == G - 1);
+                        }
+                    }
+                }
+                p.header[1] = na;
+                p.header[2] = nc3;
+            }
         }
         return;
     }
@@ -635,7 +715,16 @@ struct ScanArgs {
     const int32_t *header, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
     const char *records;
     int HQK, HV, ratio, ngroups;
+    // Segment jobs (jobs != nullptr): the grid walks entries jobs[8 (job_first + e)] =
+    // {sequence, kind, first chunk, end chunk, slot, chain steps, last} for
+    // e < header[njob_idx] instead of whole sequences. Slot buffers hold one 128 x 128
+    // fp32 matrix per (slot, v-head): S_in(1) (seg_sin), R_s (seg_r), or M_s as bf16 hi /
+    // lo units (seg_mt, kMtUnits).
+    const int32_t *jobs;
+    int job_first, njob_idx;
+    float *seg_sin, *seg_r, *seg_mt;
 };
+
 
 // LDS layouts (16-byte units). A ds_read_b128 is served in four cycles of 16 lanes: the
 // lanes of one 32-lane half whose lane bits 2, 3, 4 have equal parity; a cycle is
@@ -718,7 +807,9 @@ struct ScanBuf {
 // the next MFMA's operand: X and U tiles use token rows 32 (tt/2) + 8 (m/4) + 4 (tt%2)
 // + m%4, state tiles kt = 2s + h hold columns 32 s + 8 (m/4) + 4 h + m%4. K^T and the
 // V columns are read with the LDS transpose read.
-template <int NW>
+// SEG: the grid walks segment jobs (p.jobs); otherwise whole sequences, and none of the
+// segment code is compiled in (it costs the whole-sequence loop registers).
+template <int NW, bool SEG>
 __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, ScanBuf<NW> &BB)
 {
     constexpr int TPH = 8 / NW;  // workgroups per (sequence, v-head)
@@ -730,13 +821,31 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     const int grp = (slot / gsz) * 8 + xcd;
     if (grp >= p.ngroups)
         return;
-    const int n = p.seq_order[grp / p.HQK];
+    int n, kind = kJobFirst, cb = 0, ce = 0x7fffffff, q = -1, steps = 0, last = 0;
+    if constexpr (SEG) {
+        const int e = grp / p.HQK;
+        if (e >= p.header[p.njob_idx])
+            return;
+        const int32_t *je = p.jobs + 8 * (p.job_first + e);
+        n = je[0];
+        kind = je[1];
+        cb = je[2];
+        ce = je[3];
+        q = je[4];
+        steps = je[5];
+        last = je[6];
+    } else {
+        n = p.seq_order[grp / p.HQK];
+    }
     const int g = grp % p.HQK;
     const int h = g * p.ratio + wi / TPH;
     const int v0 = (wi % TPH) * 16 * NW;
     const int tok0 = p.seq_tok0[n], len = p.seq_len[n], c0 = p.seq_chunk0[n];
     // records exist only for chunk ids < header[0] (see the plan kernel's clamp)
     const int nck = min((len + kC - 1) / kC, max(p.header[0] - c0, 0));
+    ce = min(ce, nck);
+    const bool do_out = kind == kJobFirst || kind == kJobResume;
+    const bool vzero = kind == kJobIdent;
 
     // w is wave-uniform: LDS copy destinations (M0) are then scalar arithmetic
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
@@ -802,18 +911,20 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     struct ChunkSrc {
         __amdgpu_buffer_rsrc_t k, q, v, r;
     };
-    auto chunk_src = [&](int c) {
+    // (valid == false: empty ranges, every copy writes zeros and reads nothing)
+    auto chunk_src_v = [&](int c, bool valid) {
         const int lenc = min(kC, len - c * kC);
         ChunkSrc cs;
         cs.k = __builtin_amdgcn_make_buffer_rsrc((void *)(kbase + c * kstep), 0,
-                                                 (int)((uint32_t)(lenc - 1) * kst2 + 256u), 0x00020000);
+                                                 valid ? (int)((uint32_t)(lenc - 1) * kst2 + 256u) : 0, 0x00020000);
         cs.q = __builtin_amdgcn_make_buffer_rsrc((void *)(qbase + c * qstep), 0,
-                                                 (int)((uint32_t)(lenc - 1) * qst2 + 256u), 0x00020000);
+                                                 valid ? (int)((uint32_t)(lenc - 1) * qst2 + 256u) : 0, 0x00020000);
         cs.v = __builtin_amdgcn_make_buffer_rsrc((void *)(vbase + c * vstep), 0,
-                                                 (int)((uint32_t)(lenc - 1) * vst2 + 32u * NW), 0x00020000);
-        cs.r = __builtin_amdgcn_make_buffer_rsrc((void *)(rbase + c * rstep), 0, kRecBytes, 0x00020000);
+                                                 valid ? (int)((uint32_t)(lenc - 1) * vst2 + 32u * NW) : 0, 0x00020000);
+        cs.r = __builtin_amdgcn_make_buffer_rsrc((void *)(rbase + c * rstep), 0, valid ? kRecBytes : 0, 0x00020000);
         return cs;
     };
+    auto chunk_src = [&](int c) { return chunk_src_v(c, true); };
     auto issue_win = [&](ScanBuf<NW> &B, const ChunkSrc &cs, const int i) {
         const int win = w + NW * i;  // window kind is a compile-time function of i
         if (NW * i < 16) {
@@ -855,17 +966,129 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     const uint32_t tpoff = 16u * (lr & 7) + 128u * (lg & 1) + 256u * (lr >> 3) + 512u * (lg >> 1);
     const uint32_t goff = 32u * lg, sgoff = 4u * lr;
 
-    // ---- state: S[2 s + h] holds S[v0w + lr][32 s + 8 lg + 4 h + i], i = 0..3
-    if (nck > 0)
-        issue_chunk(BA, 0);
-    f32x4 S[8];
-    {
-        const float *sp = p.state ? p.state + n * p.st_sn + h * p.st_sh + (int64_t)(v0w + lr) * p.st_sv + 8 * lg
-                                  : nullptr;
+    // this lane's units of a slot in register-image order: S[t] at + 256 t
+    auto seg_img = [&](const float *base, int qs) {
+        return base + ((int64_t)qs * p.HV + h) * kSlotFloats + ((v0w >> 4) * 8 * 64 + l) * 4;
+    };
+    // A resumed segment with chain steps first issues the first step's M^T copy (into BB,
+    // which no chunk copy touches before the loop) and R loads, then the first chunk's copies.
+    const bool chain = SEG && steps > 0;
+    u32x4 *mb = (u32x4 *)&BB;
+    static_assert(sizeof(ScanBuf<NW>) >= 2 * kMtUnits * 16, "M^T must fit one chunk buffer");
+    constexpr int MWIN = 2 * kMtUnits / 64 / NW;  // 1 KB windows per wave
+    auto issue_m = [&](int qs) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(p.seg_mt + ((int64_t)qs * p.HV + h) * kSlotFloats), 0, 2 * kMtUnits * 16, 0x00020000);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            S[2 * s] = sp ? *(const f32x4 *)(sp + 32 * s) : f32x4{0.f, 0.f, 0.f, 0.f};
-            S[2 * s + 1] = sp ? *(const f32x4 *)(sp + 32 * s + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MWIN; ++i) {
+            const int b = w + NW * i;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GDN_LDS void *)&mb[64 * b], 16,
+                                                     16u * (uint32_t)(64 * b + l), 0, 0, 0);
+        }
+    };
+    f32x4 R[8];
+    auto load_r = [&](int qs) {
+        const float *rp = seg_img(p.seg_r, qs);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            R[t] = *(const f32x4 *)(rp + 256 * t);
+    };
+    if (chain) {
+        issue_m(q);
+        load_r(q);
+        // unconditional, so the number of operations in flight is the same on every path
+        const ChunkSrc cs = chunk_src_v(cb, ce > cb);
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            issue_win(BA, cs, i);
+    } else if (ce > cb) {
+        issue_chunk(BA, cb);
+    }
+
+    // ---- state: S[2 s + h] holds S[v0w + lr][32 s + 8 lg + 4 h + i], i = 0..3
+    f32x4 S[8];
+    // (branch on workgroup-uniform flags: a test of the per-lane pointers would make the
+    // compiler wait for each load before the next)
+    if (SEG && kind == kJobResume) {
+        const float *ip = seg_img(p.seg_sin, q);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            S[t] = *(const f32x4 *)(ip + 256 * t);
+    } else if (kind == kJobFirst && p.state) {
+        const float *sp = p.state + n * p.st_sn + h * p.st_sh + (int64_t)(v0w + lr) * p.st_sv + 8 * lg;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            S[t] = *(const f32x4 *)(sp + 32 * (t >> 1) + 4 * (t & 1));
+    } else {
+        const bool ident = SEG && kind == kJobIdent;  // row v0w + lr of the identity
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                S[t][i] = ident && 32 * (t >> 1) + 8 * lg + 4 * (t & 1) + i == v0w + lr ? 1.f : 0.f;
+    }
+
+    // ---- chain steps of a resumed segment: S <- S M_m + R_m for the slots q .. q + steps - 1.
+    // Row-wise this is S^T <- M_m^T S^T + R_m^T: an MFMA with A = M_m^T from LDS and B = the
+    // wave's own state rows, whose C layout is again the state layout (output tile t covers
+    // columns j(m) = 32 (t / 2) + 8 (m / 4) + 4 (t % 2) + m % 4). M_m and S are split into
+    // bf16 hi + lo (three products) so the chained state keeps fp32 accuracy. M_m^T is
+    // copied unit by unit into BB, which no chunk copy touches before the loop starts;
+    // LDS unit 16 j + (cu ^ kswz(j)) holds row j, k-chunk cu (the K layout of the loop).
+    if (chain) {
+        for (int m = 0; m < steps; ++m) {
+            if (m == 0) {
+                // M_q^T and R_q are in (memory operations complete in order); the first
+                // chunk's copies, at least NWIN / NW per wave, may still be in flight
+                constexpr int nv = NWIN / NW;
+                static_assert(nv < 64, "vmcnt range");
+                __builtin_amdgcn_s_waitcnt((nv & 15) | ((nv >> 4) << 14) | 0x0f70);
+                lds_barrier();
+            } else {
+                dma_barrier();  // M_m^T is in LDS, R_m in registers
+            }
+            u32x4 Bh[4], Bl[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+                split_bf16x2(S[2 * ks][0], S[2 * ks][1], h0, l0);
+                split_bf16x2(S[2 * ks][2], S[2 * ks][3], h1, l1);
+                split_bf16x2(S[2 * ks + 1][0], S[2 * ks + 1][1], h2, l2);
+                split_bf16x2(S[2 * ks + 1][2], S[2 * ks + 1][3], h3, l3);
+                Bh[ks] = u32x4{h0, h1, h2, h3};
+                Bl[ks] = u32x4{l0, l1, l2, l3};
+            }
+            auto read_a = [&](int t, u32x4 *Ah, u32x4 *Al) {
+                const int j = 32 * (t >> 1) + 8 * (lr >> 2) + 4 * (t & 1) + (lr & 3), sw = kswz(j);
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int u = 16 * j + ((4 * ks + lg) ^ sw);
+                    Ah[ks] = mb[u];
+                    Al[ks] = mb[kMtUnits + u];
+                }
+            };
+            u32x4 Ah[2][4], Al[2][4];
+            read_a(0, Ah[0], Al[0]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (t < 7)
+                    read_a(t + 1, Ah[(t + 1) & 1], Al[(t + 1) & 1]);
+                f32x4 acc = R[t];
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    acc = mfma_bf16(Ah[t & 1][ks], Bh[ks], acc);
+                    acc = mfma_bf16(Ah[t & 1][ks], Bl[ks], acc);
+                    acc = mfma_bf16(Al[t & 1][ks], Bh[ks], acc);
+                }
+                S[t] = acc;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (m + 1 < steps) {
+                lds_barrier();  // every wave is done with M_m^T
+                issue_m(q + m + 1);
+                load_r(q + m + 1);
+            }
         }
     }
 
@@ -922,6 +1145,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 for (int tt = 0; tt < 4; ++tt) {  // (b)'s operands
                     const int trow = 32 * (tt >> 1) + 4 * (tt & 1);
                     vv[tt] = lds_tr16(Vb + voff + 32 * NW * trow);
+                    if (vzero)
+                        vv[tt] = u32x2{0u, 0u};
                     gm[tt] = *(const f32x4 *)(Gb + goff + 4 * trow);
                 }
             }
@@ -1022,6 +1247,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
             }
         };
         u32x4 kt[2][2];
+        if (!do_out)
+            ktRead(0, kt[0]);  // (f)'s first operands
         // Tile tt's combine and store run after tile tt + 1's MFMAs are issued, so they
         // never wait on the MFMA chain that produced them.
         f32x4 Oi[2], Oa[2];
@@ -1035,6 +1262,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         };
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
+            if (!do_out)
+                break;
             __builtin_amdgcn_sched_barrier(0);
             const int cb = tt & 1;
             if (tt < 3)
@@ -1067,22 +1296,67 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 acc = mfma_bf16(kt[gidx & 1][sp], Wh[sp], acc);
                 acc = mfma_bf16(kt[gidx & 1][sp], Wl[sp], acc);
             }
-            if (gidx == 0)
+            if (gidx == 0 && do_out)
                 out_epi(3);
             S[gidx] = acc;
         }
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    for (int c = 0; c < nck; c += 2) {
+    for (int c = cb; c < ce; c += 2) {
         dma_barrier();  // chunk c is in BA; every wave is done with BB
-        compute(BA, c, BB, c + 1 < nck);
-        if (c + 1 >= nck)
+        compute(BA, c, BB, c + 1 < ce);
+        if (c + 1 >= ce)
             break;
         dma_barrier();
-        compute(BB, c + 1, BA, c + 2 < nck);
+        compute(BB, c + 1, BA, c + 2 < ce);
     }
 
+    if (SEG && kind == kJobResume && !last)
+        return;
+    if (SEG && kind == kJobIdent) {
+        // This wave holds rows k = v0w .. v0w + 15 of M_s, i.e. k-chunks cu0 and cu0 + 1 of
+        // every row j of M_s^T. Transpose them through a per-wave LDS stage (fp32, row j at
+        // 64 j bytes) in the chunk buffer the last chunk did not use (free since the last
+        // chunk's barrier), then write each unit split into bf16 hi and lo; the two units of
+        // one j are adjacent (cu0 is even), so lane pairs write 32 contiguous bytes.
+        float *stg = (float *)(((ce - cb) & 1) ? (void *)&BB : (void *)&BA) + 2048 * w;
+        static_assert(sizeof(ScanBuf<NW>) >= NW * 2048 * 4, "stage must fit one chunk buffer");
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    stg[(32 * s + 8 * lg + 4 * hh + i) * 16 + lr] = S[2 * s + hh][i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        u32x4 *mt = (u32x4 *)(p.seg_mt + ((int64_t)q * p.HV + h) * kSlotFloats);
+        const int cu0 = v0w >> 3;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int u = l + 64 * r, j = u >> 1, c2 = u & 1;
+            const f32x4 a = *(const f32x4 *)(stg + 16 * j + 8 * c2);
+            const f32x4 b = *(const f32x4 *)(stg + 16 * j + 8 * c2 + 4);
+            uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+            split_bf16x2(a[0], a[1], h0, l0);
+            split_bf16x2(a[2], a[3], h1, l1);
+            split_bf16x2(b[0], b[1], h2, l2);
+            split_bf16x2(b[2], b[3], h3, l3);
+            const int un = 16 * j + ((cu0 + c2) ^ kswz(j));
+            mt[un] = u32x4{h0, h1, h2, h3};
+            mt[kMtUnits + un] = u32x4{l0, l1, l2, l3};
+        }
+        return;
+    }
+    if (SEG && (kind == kJobZero || (kind == kJobFirst && q >= 0))) {  // R_s or S_in(1)
+        float *ip = (float *)seg_img(kind == kJobZero ? p.seg_r : p.seg_sin, q);
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            *(f32x4 *)(ip + 256 * t) = S[t];
+        return;
+    }
     float *np = p.new_state + n * p.ns_sn + h * p.ns_sh + (int64_t)(v0w + lr) * p.ns_sv + 8 * lg;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -1091,16 +1365,18 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     }
 }
 
+template <bool SEG>
 __global__ __launch_bounds__(512) void gdn_prefill_scan8_kernel(ScanArgs p)
 {
     __shared__ ScanBuf<8> bufA, bufB;
-    scan_body<8>(p, bufA, bufB);
+    scan_body<8, SEG>(p, bufA, bufB);
 }
 
+template <bool SEG>
 __global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p)
 {
     __shared__ ScanBuf<4> bufA, bufB;
-    scan_body<4>(p, bufA, bufB);
+    scan_body<4, SEG>(p, bufA, bufB);
 }
 
 }  // namespace gdn
@@ -1115,15 +1391,34 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 int64_t max_chunks(int64_t T, int64_t N) { return (T + kChunkH - 1) / kChunkH + N; }
 
+// Segments per sequence (the default variant only): when (sequence, v-head) pairs are too
+// few to fill 256 CUs, the largest G <= 8 whose pass-A jobs N HV (2 G - 3) still fit one
+// workgroup per CU; 1 means no segments (G = 2 would scan its halves one after the other).
+int seg_count(int64_t T, int64_t N, int64_t HV)
+{
+    if (T <= 0 || N <= 0 || N * HV * 3 > 256)
+        return 1;
+    int G = 3;
+    while (G < 8 && N * HV * (2 * (G + 1) - 3) <= 256)
+        ++G;
+    return G;
+}
+
 struct Layout {
     int64_t nc;
     int64_t header, chunk_tok0, chunk_len, seq_chunk0, seq_order, seq_tok0, seq_len, records,
         total;
+    int G;                // segments per sequence at most (1: none)
+    int64_t capA, capC;   // pass A / pass C job capacity
+    int64_t jobs, seg_sin, seg_r, seg_mt;
 };
 
 Layout layout(int64_t T, int64_t N, int64_t HV)
 {
     Layout L;
+    L.G = seg_count(T, N, HV);
+    L.capA = N * (2 * L.G - 3);
+    L.capC = N * (L.G - 1);
     L.nc = max_chunks(T, N);
     int64_t o = 0;
     L.header = o;
@@ -1141,7 +1436,18 @@ Layout layout(int64_t T, int64_t N, int64_t HV)
     L.seq_len = o;
     o += N * 4;
     L.records = align256(o);
-    L.total = L.records + L.nc * HV * gdn::kRecBytes;
+    o = L.records + L.nc * HV * gdn::kRecBytes;
+    L.jobs = L.seg_sin = L.seg_r = L.seg_mt = 0;
+    if (L.G > 1) {
+        const int64_t slot_bytes = N * (L.G - 1) * HV * gdn::kSlotFloats * 4;
+        L.jobs = align256(o);
+        o = L.jobs + (L.capA + L.capC) * 8 * 4;
+        L.seg_sin = align256(o);
+        L.seg_r = L.seg_sin + slot_bytes;
+        L.seg_mt = L.seg_r + slot_bytes;
+        o = L.seg_mt + slot_bytes;
+    }
+    L.total = o;
     return L;
 }
 
@@ -1267,6 +1573,11 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     pa.out = (gdn::bf16_t *)p->output;
     pa.o_st = p->output_stride[0];
     pa.o_sh = p->output_stride[1];
+    // segments only for the default variant (the tuning variants keep whole sequences)
+    const int G = p->variant == 0 ? L.G : 1;
+    pa.seg_G = G;
+    pa.seg_capA = (int)L.capA;
+    pa.jobs = G > 1 ? (int32_t *)(ws + L.jobs) : nullptr;
     hipLaunchKernelGGL(gdn::gdn_prefill_plan_kernel, dim3(1 + kZeroFillBlocks), dim3(256), 0,
                        st, pa);
     int rc = gdn_check_launch("gdn_prefill_plan_kernel");
@@ -1347,23 +1658,50 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         sa.HQK = HQK;
         sa.HV = HV;
         sa.ratio = ratio;
-        const int64_t ngroups = (int64_t)N * HQK;
-        sa.ngroups = (int)ngroups;
+        sa.jobs = nullptr;
+        sa.job_first = 0;
+        sa.njob_idx = 0;
+        sa.seg_sin = G > 1 ? (float *)(ws + L.seg_sin) : nullptr;
+        sa.seg_r = G > 1 ? (float *)(ws + L.seg_r) : nullptr;
+        sa.seg_mt = G > 1 ? (float *)(ws + L.seg_mt) : nullptr;
         // 8 waves per workgroup = one (sequence, v-head) each, two waves per SIMD; with
         // few (sequence, v-head) pairs, 4 waves and two workgroups per pair spread the
         // state rows over twice as many CUs. variant: 1 forces 4 waves, 2 forces 8.
-        const bool nw4 = p->variant == 1 || (p->variant != 2 && (int64_t)N * HV <= 128);
-        const int tph = nw4 ? 2 : 1;
-        const int64_t blocks = 8 * ((int64_t)tph * ratio) * ((ngroups + 7) / 8);
-        if (ngroups > 0x7fffffff || blocks > 0x7fffffff)
-            return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
-        if (nw4)
-            hipLaunchKernelGGL(gdn::gdn_prefill_scan4_kernel, dim3((unsigned)blocks), dim3(256),
-                               0, st, sa);
-        else
-            hipLaunchKernelGGL(gdn::gdn_prefill_scan8_kernel, dim3((unsigned)blocks), dim3(512),
-                               0, st, sa);
-        rc = gdn_check_launch("gdn_prefill_scan_kernel");
+        auto scan = [&](int64_t units, bool nw4) {
+            const int64_t ngroups = units * HQK;
+            sa.ngroups = (int)ngroups;
+            const int tph = nw4 ? 2 : 1;
+            const int64_t blocks = 8 * ((int64_t)tph * ratio) * ((ngroups + 7) / 8);
+            if (ngroups > 0x7fffffff || blocks > 0x7fffffff)
+                return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
+            const dim3 grid((unsigned)blocks), b4(256), b8(512);
+            if (sa.jobs && nw4)
+                hipLaunchKernelGGL(gdn::gdn_prefill_scan4_kernel<true>, grid, b4, 0, st, sa);
+            else if (sa.jobs)
+                hipLaunchKernelGGL(gdn::gdn_prefill_scan8_kernel<true>, grid, b8, 0, st, sa);
+            else if (nw4)
+                hipLaunchKernelGGL(gdn::gdn_prefill_scan4_kernel<false>, grid, b4, 0, st, sa);
+            else
+                hipLaunchKernelGGL(gdn::gdn_prefill_scan8_kernel<false>, grid, b8, 0, st, sa);
+            return gdn_check_launch("gdn_prefill_scan_kernel");
+        };
+        if (G > 1) {
+            // pass A: segment 0 of every sequence and both state maps of the middle segments
+            sa.jobs = pa.jobs;
+            sa.job_first = 0;
+            sa.njob_idx = 1;
+            rc = scan(L.capA, false);
+            if (rc)
+                return rc;
+            // pass C: outputs of segments 1 .. G - 1, each chaining its entering state first;
+            // the last segment's final state is new_state
+            sa.job_first = (int)L.capA;
+            sa.njob_idx = 2;
+            rc = scan(L.capC, L.capC * HV <= 128);
+        } else {
+            const bool nw4 = p->variant == 1 || (p->variant != 2 && (int64_t)N * HV <= 128);
+            rc = scan(N, nw4);
+        }
         if (rc)
             return rc;
     }

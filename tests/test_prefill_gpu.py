@@ -211,3 +211,38 @@ def test_prefill_gap_before_first_sequence(dev, nseq):
     inp = prefill_inputs(lens, hqk=4, hv=8, seed=31, with_state=True, pad_tokens=53)
     inp.cu_seqlens = inp.cu_seqlens + 37  # 37 leading and 16 trailing gap tokens
     _run(dev, inp, f"lead gap N={nseq}")
+
+
+@pytest.mark.parametrize("gates", ["strong", "mild", "none"])
+def test_prefill_segments_long_memory(dev, gates):
+    """Few (sequence, v-head) pairs: each long sequence is scanned as parallel segments
+    whose states are chained (S_in M + R). Mild or no decay makes every segment's state
+    carry into the next one."""
+    _run(dev, prefill_inputs([2048], seed=41, with_state=True, gates=gates, state_std=0.1),
+         f"segments gates={gates}")
+
+
+@pytest.mark.parametrize("lens,hqk,hv", [([1500, 300], 16, 32), ([3000], 4, 8),
+                                         ([900, 0, 1400, 65], 4, 8)])
+def test_prefill_segments_mixed(dev, lens, hqk, hv):
+    """Segmented and whole sequences in one call (short ones are not split), up to eight
+    segments per sequence, empty sequences."""
+    _run(dev, prefill_inputs(lens, hqk=hqk, hv=hv, seed=43, with_state=True, gates="mild",
+                             state_std=0.05), f"segments lens={lens}")
+
+
+def test_prefill_segments_match_whole_sequence_scan(dev):
+    """The segmented scan and the whole-sequence scan (tuning variant 2) agree."""
+    from gdn_hip.api import set_prefill_variant
+    inp = prefill_inputs([1800], seed=47, with_state=True, gates="mild").to(dev)
+    out_s, ns_s = gdn_prefill(*inp.args())
+    try:
+        set_prefill_variant(2)
+        out_w, ns_w = gdn_prefill(*inp.args())
+    finally:
+        set_prefill_variant(0)
+    torch.cuda.synchronize()
+    vo = check_output(out_s, out_w.float())
+    vs = check_state(ns_s, ns_w)
+    print(f"[segmented vs whole] output {vo} | state {vs}", flush=True)
+    assert vo.ok and vs.ok
