@@ -37,9 +37,21 @@ __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c)
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c)
+// A lone 4-slot term as a 16x16x32 MFMA with zero upper halves (a 16x16x16 MFMA costs the
+// same ~16.7 cycles on gfx950)
+__device__ __forceinline__ f32x4 mfma_bf16_k16(u32x2 a, u32x2 b, f32x4 c)
 {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    return mfma_bf16(u32x4{a[0], a[1], 0u, 0u}, u32x4{b[0], b[1], 0u, 0u}, c);
+}
+
+// Four floats split into bf16 hi / lo: {hi(v0, v1), hi(v2, v3), lo(v0, v1), lo(v2, v3)}, so
+// .xy is a 4-element hi operand and the whole vector an 8-element [hi | lo] operand.
+__device__ __forceinline__ u32x4 split4(f32x4 v)
+{
+    uint32_t h01, l01, h23, l23;
+    split_bf16x2(v[0], v[1], h01, l01);
+    split_bf16x2(v[2], v[3], h23, l23);
+    return u32x4{h01, h23, l01, l23};
 }
 
 constexpr int kC = 64;   // chunk length
@@ -384,8 +396,8 @@ struct PrepSmem {
     float L[2][VH][64];   // L by token
     float LT[2][VH][64];  // L of token 16 b + 4 i + g at 16 b + 4 g + i
     float B[2][VH][64];   // beta by token
-    f32x4 XA[VH][4][64];  // X_w in A-operand layout, by lane
-    f32x4 AO[VH][6][64];  // off-diagonal A_im (m < i) in A-operand layout, by lane; i(i-1)/2 + m
+    u32x4 XA[VH][4][64];  // X_w in A-operand layout, by lane, split4
+    u32x4 AO[VH][6][64];  // off-diagonal A_im (m < i) as XA; index i(i-1)/2 + m
     float Ms[4 * VH][16][16];  // per wave: -A_ww rows, X_w, then T' staging
 };
 
@@ -550,7 +562,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 if (i == w)
                     Aww = av;
                 else
-                    sm.AO[hv][i * (i - 1) / 2 + w][l] = av;
+                    sm.AO[hv][i * (i - 1) / 2 + w][l] = split4(av);
             }
         }
 
@@ -585,7 +597,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 #undef GDN_SUBST_STEP
             xw = f32x4{x[0], x[1], x[2], x[3]};
         }
-        sm.XA[hv][w][l] = xw;
+        sm.XA[hv][w][l] = split4(xw);
         // X_w in B-operand layout (lane (n, lg) element s = X[4 s + lg][n]) via the scratch
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
@@ -599,25 +611,43 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
             copy(N, true, sm.Q);
 
         // Column block w of T; TB[i] = T_(w+i),w in B-operand layout.
+        // T_iw = -X_i z, z = sum_m A_im T_mw, with every 16x16x16 block product split into
+        // bf16 hi / lo terms a_h b_h + a_l b_h + a_h b_l (a_l b_l, ~2^-16 relative, dropped).
+        // An MFMA only pairs lane (m, g)'s k-slot j of A with lane (n, g)'s k-slot j of B, so
+        // the fp32 operand layouts carry over (slot j = column 4 j + g), and a 16x16x32 MFMA
+        // with A = [a_h | a_l], B = [b_h | b_h] computes two terms: column 0 takes 16 bf16
+        // MFMAs instead of 36 fp32 ones at twice their cost.
+        u32x4 TS[4];
+        TS[0] = split4(TB[0]);
 #pragma unroll
         for (int i = 1; i < 4; ++i) {
             if (i + w > 3)
                 break;
-            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            u32x4 as[3];
 #pragma unroll
             for (int m = 0; m < i; ++m) {  // A block (i + w, m + w)
                 const int ii = i + w, mm = m + w;
-                const f32x4 a = sm.AO[hv][ii * (ii - 1) / 2 + mm][l];
-#pragma unroll
-                for (int s2 = 0; s2 < 4; ++s2)
-                    z = mfma_f32(a[s2], TB[m][s2], z);
+                as[m] = sm.AO[hv][ii * (ii - 1) / 2 + mm][l];
             }
-            const f32x4 xa = sm.XA[hv][i + w][l];
-            f32x4 t = {0.f, 0.f, 0.f, 0.f};
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2)
-                t = mfma_f32(xa[s2], z[s2], t);
+            for (int m = 0; m < i; ++m)
+                z = mfma_bf16(as[m], u32x4{TS[m][0], TS[m][1], TS[m][0], TS[m][1]}, z);
+#pragma unroll
+            for (int m = 0; m < i; m += 2) {
+                if (m + 1 < i)
+                    z = mfma_bf16(u32x4{as[m][0], as[m][1], as[m + 1][0], as[m + 1][1]},
+                                  u32x4{TS[m][2], TS[m][3], TS[m + 1][2], TS[m + 1][3]}, z);
+                else
+                    z = mfma_bf16_k16(u32x2{as[m][0], as[m][1]}, u32x2{TS[m][2], TS[m][3]}, z);
+            }
+            const u32x4 xs = sm.XA[hv][i + w][l];
+            const u32x4 zs = split4(z);
+            f32x4 t = mfma_bf16(xs, u32x4{zs[0], zs[1], zs[0], zs[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
+            t = mfma_bf16_k16(u32x2{xs[0], xs[1]}, u32x2{zs[2], zs[3]}, t);
             TB[i] = -t;
+            if (i + w < 3)
+                TS[i] = split4(TB[i]);
         }
 
         // T' = T diag(beta) -> record (bf16 hi / lo, block layout), one block at a time
