@@ -44,6 +44,12 @@ __device__ __forceinline__ f32x4 mfma_bf16_k16(u32x2 a, u32x2 b, f32x4 c)
     return mfma_bf16(u32x4{a[0], a[1], 0u, 0u}, u32x4{b[0], b[1], 0u, 0u}, c);
 }
 
+// v if bit b of the lane's mask is set, else +0 (sign-extended bit field as an AND mask)
+__device__ __forceinline__ float keep_if(float v, int bits, int b)
+{
+    return __int_as_float(__float_as_int(v) & __builtin_amdgcn_sbfe(bits, b, 1));
+}
+
 // Four floats split into bf16 hi / lo: {hi(v0, v1), hi(v2, v3), lo(v0, v1), lo(v2, v3)}, so
 // .xy is a 4-element hi operand and the whole vector an 8-element [hi | lo] operand.
 __device__ __forceinline__ u32x4 split4(f32x4 v)
@@ -486,10 +492,23 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     };
     float (*Ms)[16] = sm.Ms[wv];
 
+    // Diagonal-block masks of this lane, one bit per element: bits 0..3 keep P'[t][j] for
+    // j <= t (t = 16 w + lr, j = 16 w + 4 lg + e), bits 4..7 keep A[t][j] for j < t
+    // (t = 16 w + pi(lr), j = 16 w + 4 e + lg). They do not depend on w.
+    int dbits0 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        dbits0 |= (4 * lg + e <= lr) << e;
+        dbits0 |= (4 * e + lg < pi16(lr)) << (4 + e);
+    }
     auto compute = [&](const Unit &U, const u32x4 *Kb, int buf, float &na, float &nb,
                        const Unit &N, bool more) {
         char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
         const float *Ls = sm.L[buf][hv], *Bs = sm.B[buf][hv], *LsT = sm.LT[buf][hv];
+        // re-derived per unit, so the compiler keeps one register instead of hoisting a
+        // lane mask per element out of the unit loop (they spilled to VGPR lanes)
+        int dbits = dbits0;
+        asm volatile("" : "+v"(dbits));
 
         // P' row block w: lane (t = 16 w + lr, lg) holds columns 16 jb + 4 lg .. +3. All
         // blocks' MFMAs issue before any scaling / store, which then never waits on them.
@@ -517,10 +536,12 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 const f32x4 Lj = *(const f32x4 *)&Ls[16 * jb + 4 * lg];
                 float pv[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 16 * jb + 4 * lg + e;
-                    const float v = p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * rp[jb][e];
-                    pv[e] = (jb < w || j <= t) ? v : 0.f;  // only the diagonal block is masked
+                for (int e = 0; e < 4; ++e)
+                    pv[e] = p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * rp[jb][e];
+                if (jb == w) {  // diagonal block: zero above the diagonal
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        pv[e] = keep_if(pv[e], dbits, e);
                 }
                 *(u32x2 *)(rec + kRecP + 2 * (tri_blk(w, jb) * kBlk + lr * 16 + 4 * lg)) =
                     u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
@@ -554,14 +575,14 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 const float Lt = Ls[t], btt = Bs[t];
                 f32x4 av;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 16 * w + 4 * e + lg;
-                    const float v = btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * ra[i][e];
-                    av[e] = (w < i || j < t) ? v : 0.f;  // only the diagonal block is masked
-                }
-                if (i == w)
+                for (int e = 0; e < 4; ++e)
+                    av[e] = btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * ra[i][e];
+                if (i == w) {  // diagonal block: strictly lower part only
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        av[e] = keep_if(av[e], dbits, 4 + e);
                     Aww = av;
-                else
+                } else
                     sm.AO[hv][i * (i - 1) / 2 + w][l] = split4(av);
             }
         }
