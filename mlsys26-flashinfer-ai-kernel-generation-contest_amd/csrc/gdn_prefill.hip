@@ -142,7 +142,13 @@ constexpr int kJobResume = 3;  // from S_in(1) and (steps) chain steps; outputs;
 //   16 j + (cu ^ kswz(j)) holds M_s[8 cu .. 8 cu + 7][j].
 constexpr int64_t kSlotFloats = 128 * 128;
 constexpr int kMtUnits = 2048;
-constexpr int kSegMinChunks = 4;            // shortest segment
+constexpr int kSegMinChunks = 4;            // shortest segment (before balancing)
+// Segment lengths balance the two passes (measured on MI355X): a segment-0 chunk, which
+// writes outputs in pass A, costs ~1/0.83 of a state-map chunk, and each chain step
+// delays a pass-C segment by ~0.9 chunk-times, so segment s >= 1 gets 0.9 (s - 1) chunks
+// fewer than segment 1.
+constexpr float kSegFirstWeight = 0.83f;
+constexpr float kSegChainChunks = 0.9f;
 
 // ------------------------------------------------------------------------- plan
 struct PlanArgs {
@@ -286,14 +292,31 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                         G = Ls > 0 ? (ncks + Ls - 1) / Ls : 1;
                         if (G < 3)
                             G = 1;  // two segments would run one after the other
+                        // boundary of segment sg: balanced lengths (see kSegFirstWeight) when
+                        // every segment keeps at least 2 chunks, else equal lengths
+                        const float base = (ncks + kSegChainChunks * (G - 1) * (G - 2) / 2) /
+                                           (kSegFirstWeight + G - 1);
+                        const bool bal = G > 1 && base - kSegChainChunks * (G - 2) >= 2.f &&
+                                         kSegFirstWeight * base >= 2.f;
+                        auto bnd = [&](int sg) {
+                            if (sg >= G)
+                                return ncks;
+                            if (!bal)
+                                return min(sg * Ls, ncks);
+                            // chunks before segment sg: kSegFirstWeight base + sum over
+                            // u = 1 .. sg - 1 of (base - kSegChainChunks (u - 1))
+                            const float x = kSegFirstWeight * base + (sg - 1) * base -
+                                            kSegChainChunks * (sg - 1) * (sg - 2) / 2;
+                            return min(max((int)(x + 0.5f), sg), ncks);
+                        };
                         const int q = G > 1 ? qs : -1;
                         qs += G - 1;
                         if (pass == 0) {
-                            put(na++, n, kJobFirst, 0, G > 1 ? Ls : ncks, q, 0, 0);
+                            put(na++, n, kJobFirst, 0, G > 1 ? bnd(1) : ncks, q, 0, 0);
                             continue;
                         }
                         for (int sg = 1; sg < G; ++sg) {
-                            const int cb = sg * Ls, ce = min(cb + Ls, ncks);
+                            const int cb = bnd(sg), ce = bnd(sg + 1);
                             if (sg < G - 1) {
                                 put(na++, n, kJobZero, cb, ce, q + sg - 1, 0, 0);
                                 put(na++, n, kJobIdent, cb, ce, q + sg - 1, 0, 0);
