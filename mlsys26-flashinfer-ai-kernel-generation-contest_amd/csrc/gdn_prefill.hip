@@ -86,6 +86,19 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Barrier over LDS that leaves buffer_load ... lds copies in flight. Those copies write LDS
+// and count in vmcnt, so the LDS release fence of lds_barrier waits for every one of them
+// (vmcnt(0)); where the copies in flight target a buffer nobody reads before a later
+// dma_barrier, waiting for this wave's own LDS operations (lgkmcnt(0)) is enough. The
+// empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier_inflight()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt not waited for
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // DPP move with a row / bank mask: disabled rows and out-of-row sources read 0.
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp_or0(float x)
@@ -650,7 +663,9 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
             TB[0][s2] = Ms[4 * s2 + lg][lr];
-        lds_barrier();  // every X_i is in XA, every A_im in AO; every wave is done with Q
+        // every X_i is in XA, every A_im in AO; every wave is done with Q (the next unit's K
+        // copy stays in flight)
+        lds_barrier_inflight();
         if (more)
             copy(N, true, sm.Q);
 
@@ -1117,7 +1132,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 constexpr int nv = NWIN / NW;
                 static_assert(nv < 64, "vmcnt range");
                 __builtin_amdgcn_s_waitcnt((nv & 15) | ((nv >> 4) << 14) | 0x0f70);
-                lds_barrier();
+                lds_barrier_inflight();
             } else {
                 dma_barrier();  // M_m^T is in LDS, R_m in registers
             }
@@ -1159,7 +1174,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
             }
             __builtin_amdgcn_sched_barrier(0);
             if (m + 1 < steps) {
-                lds_barrier();  // every wave is done with M_m^T
+                lds_barrier_inflight();  // every wave is done with M_m^T
                 issue_m(q + m + 1);
                 load_r(q + m + 1);
             }
