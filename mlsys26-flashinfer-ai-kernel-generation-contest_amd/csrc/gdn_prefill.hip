@@ -488,12 +488,15 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     // Gates (gdn_decode/solution/triton/kernel.py:128-131); padding tokens: alpha = 1,
     // beta = 0. Cumulative decay in log2 units: every factor below is 2^(non-positive
     // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow).
-    auto gate_in = [&](const Unit &U, float &a_in, float &b_in) {
+    // The raw bf16 bits are kept until gates() converts them at the end of the unit: a
+    // conversion here would make the gate wave wait for these loads at the unit's start.
+    auto gate_in = [&](const Unit &U, uint32_t &a_in, uint32_t &b_in) {
         const int tl = U.tok0 + min(l, U.len - 1);
-        a_in = bf16_to_f32(p.a[(int64_t)tl * p.a_st + (int64_t)U.h * p.a_sh]);
-        b_in = bf16_to_f32(p.b[(int64_t)tl * p.b_st + (int64_t)U.h * p.b_sh]);
+        a_in = p.a[(int64_t)tl * p.a_st + (int64_t)U.h * p.a_sh];
+        b_in = p.b[(int64_t)tl * p.b_st + (int64_t)U.h * p.b_sh];
     };
-    auto gates = [&](const Unit &U, float a_in, float b_in, int buf) {
+    auto gates = [&](const Unit &U, uint32_t a_raw, uint32_t b_raw, int buf) {
+        const float a_in = bf16_to_f32(a_raw), b_in = bf16_to_f32(b_raw);
         // log2 alpha = -exp(A_log) log2(1 + e^x) (x > 20: -exp(A_log) x log2 e), with the
         // hardware base-2 exp / log; beta = 1 / (1 + e^-b)
         constexpr float kLog2e = 1.44269504088896340736f;
@@ -537,7 +540,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         dbits0 |= (4 * lg + e <= lr) << e;
         dbits0 |= (4 * e + lg < pi16(lr)) << (4 + e);
     }
-    auto compute = [&](const Unit &U, const u32x4 *Kb, int buf, float &na, float &nb,
+    auto compute = [&](const Unit &U, const u32x4 *Kb, int buf, uint32_t &na, uint32_t &nb,
                        const Unit &N, bool more) {
         char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
         const float *Ls = sm.L[buf][hv], *Bs = sm.B[buf][hv], *LsT = sm.LT[buf][hv];
@@ -738,7 +741,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     if (u >= nunits)
         return;
     Unit U = unit(u);
-    float a_in = 0.f, b_in = 0.f;
+    uint32_t a_in = 0, b_in = 0;
     copy(U, false, sm.K[0]);
     copy(U, true, sm.Q);
     if (w == kGateWave) {
