@@ -1,0 +1,313 @@
+// Packed variable-length Gated DeltaNet prefill for gfx950: chunked WY/UT form,
+// C = 64 tokens per chunk, bf16 MFMA with fp32 accumulation.
+//
+// Per chunk of one sequence and v-head h (q/k head g = h / ratio), with start
+// state S0 (k-last, S[v,k]) and L_t = sum_{i<=t} log alpha_i inside the chunk:
+//   A[t,j] = beta_t exp(L_t - L_j) (k_t . k_j)  (j < t),    T = (I + A)^-1
+//   U      = T (beta * (V - exp(L) * (K S0^T)))               (pseudo-values)
+//   O      = scale * (exp(L) * (Q S0^T) + P U),  P[t,j] = exp(L_t - L_j) (q_t . k_j), j <= t
+//   S_end  = exp(L_C) S0 + (exp(L_C - L) * U)^T K
+// (gdn_prefill/solution/triton/kernel.py:60-79; Yang et al. 2024, "Parallelizing
+// Linear Transformers with the Delta Rule over Sequence Length" / "Gated Delta
+// Networks"). Only non-positive log differences are exponentiated, so strong
+// decay underflows to 0 instead of overflowing; no clamping.
+//
+// Three launches on the caller's stream:
+//   plan  (1 + Z workgroups): sequence -> chunk tables from cu_seqlens on the
+//         device (no host sync), longest-first sequence order, and zero-fill of
+//         output rows that belong to no sequence.
+//   prep  (chunks x q/k heads): K K^T and Q K^T on MFMA, gates, cumulative log
+//         decay, T = (I + A)^-1 (16x16 diagonal blocks by fp32 substitution,
+//         off-diagonal blocks on split-bf16 MFMA), P; writes per (chunk, v-head) records.
+//   scan  (sequences x v-heads): one workgroup owns 16 NW state rows of one
+//         (sequence, v-head) and walks its chunks in order, state in registers.
+//         fp32-valued operands on the state path (S0, R, T, U) are split into bf16
+//         hi + lo halves so the state keeps ~2^-16 relative accuracy. With few
+//         sequences, long ones are cut into segments scanned in parallel (two scan
+//         launches over job tables).
+//
+// Files: gdn_prefill.h (records, layouts, argument structs, shared helpers),
+// gdn_prefill_plan.hip, gdn_prefill_prep.hip, gdn_prefill_scan.hip (the kernels) and
+// gdn_prefill.hip (workspace layout and launches behind gdn_prefill_launch).
+#pragma once
+
+#include "gdn_common.h"
+
+namespace gdn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// A lone 4-slot term as a 16x16x32 MFMA with zero upper halves (a 16x16x16 MFMA costs the
+// same ~16.7 cycles on gfx950)
+__device__ __forceinline__ f32x4 mfma_bf16_k16(u32x2 a, u32x2 b, f32x4 c)
+{
+    return mfma_bf16(u32x4{a[0], a[1], 0u, 0u}, u32x4{b[0], b[1], 0u, 0u}, c);
+}
+
+// v if bit b of the lane's mask is set, else +0 (sign-extended bit field as an AND mask)
+__device__ __forceinline__ float keep_if(float v, int bits, int b)
+{
+    return __int_as_float(__float_as_int(v) & __builtin_amdgcn_sbfe(bits, b, 1));
+}
+
+// Four floats split into bf16 hi / lo: {hi(v0, v1), hi(v2, v3), lo(v0, v1), lo(v2, v3)}, so
+// .xy is a 4-element hi operand and the whole vector an 8-element [hi | lo] operand.
+__device__ __forceinline__ u32x4 split4(f32x4 v)
+{
+    uint32_t h01, l01, h23, l23;
+    split_bf16x2(v[0], v[1], h01, l01);
+    split_bf16x2(v[2], v[3], h23, l23);
+    return u32x4{h01, h23, l01, l23};
+}
+
+constexpr int kC = 64;   // chunk length
+constexpr int kDK = 128; // head size
+
+// Per (chunk, v-head) record in the workspace. 64x64 lower-triangular matrices are
+// stored as their 10 lower 16x16 blocks, block (i, j <= i) at index i(i+1)/2 + j,
+// each block row-major: exactly the rows and 8-column runs an MFMA A operand reads.
+constexpr int kBlk = 256;        // elements per 16x16 block
+// Byte offsets:
+constexpr int kRecThi = 0;       // bf16 [10][16][16]  T' = (I + A)^-1 diag(beta), high half
+constexpr int kRecTlo = 5120;    // bf16 [10][16][16]  low half
+constexpr int kRecP = 10240;     // bf16 [10][16][16]  P' = scale * P (decayed, causal Q K^T)
+constexpr int kRecGates = 15360; // f32 gamma[64], dec[64], scale * gamma[64], gammaC
+constexpr int kRecZero = 16256;  // 16 zero bytes (after the gates): what absent blocks read
+constexpr int kRecBytes = 16384;
+
+__device__ __forceinline__ int tri_blk(int i, int j) { return i * (i + 1) / 2 + j; }
+
+// Workgroup barrier that orders LDS only: global loads issued before it (the next
+// chunk's prefetch) stay in flight across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Barrier over LDS that leaves buffer_load ... lds copies in flight. Those copies write LDS
+// and count in vmcnt, so the LDS release fence of lds_barrier waits for every one of them
+// (vmcnt(0)); where the copies in flight target a buffer nobody reads before a later
+// dma_barrier, waiting for this wave's own LDS operations (lgkmcnt(0)) is enough. The
+// empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier_inflight()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt not waited for
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// DPP move with a row / bank mask: disabled rows and out-of-row sources read 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_or0(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xF, true));
+}
+
+// Inclusive prefix sum over the 64 lanes: shifts by 1, 2, 4, 8 inside each 16-lane row,
+// then row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then the total of
+// rows 0-1 into rows 2-3 (row_bcast:31).
+__device__ __forceinline__ float wave_prefix_sum(float x)
+{
+    x += dpp_or0<0x111, 0xF>(x);
+    x += dpp_or0<0x112, 0xF>(x);
+    x += dpp_or0<0x114, 0xF>(x);
+    x += dpp_or0<0x118, 0xF>(x);
+    x += dpp_or0<0x142, 0xA>(x);
+    x += dpp_or0<0x143, 0xC>(x);
+    return x;
+}
+
+template <int K>
+__device__ __forceinline__ float quad_bcast(float x)
+{
+    return dpp_mov<K | (K << 2) | (K << 4) | (K << 6)>(x);
+}
+
+__device__ __forceinline__ int64_t load_cu(const void *cu, int cu64, int i)
+{
+    return cu64 ? ((const int64_t *)cu)[i] : (int64_t)((const int32_t *)cu)[i];
+}
+
+// Segment jobs. When (sequence, v-head) pairs are too few to fill the GPU, a long sequence
+// is cut into G segments scanned in parallel. The state map of a segment is affine,
+// S_out = S_in M_s + R_s. Pass A scans segment 0 from the true initial state, giving
+// S_in(1), and every middle segment s = 1 .. G - 2 twice from known states: value rows from
+// zero give R_s, identity rows with V = 0 give M_s. Pass C rescans each segment s >= 1 for
+// its outputs; its workgroups first chain S_in(s) = S_in(1) M_1 + R_1 ... (s - 1 steps) on
+// their own state rows, and the last segment's scan ends in the final state, so the last
+// segment needs no state map.
+constexpr int kJobFirst = 0;   // from the initial state; outputs; final state -> new_state,
+                               // or (slot >= 0) -> S_in(1)
+constexpr int kJobZero = 1;    // value rows from a zero state, no outputs: final state = R_s
+constexpr int kJobIdent = 2;   // identity rows with V = 0, no outputs: final state = M_s,
+                               // stored as bf16 hi / lo units of M^T
+constexpr int kJobResume = 3;  // from S_in(1) and (steps) chain steps; outputs; final state
+                               // -> new_state for the last segment
+// Slots hold one 128 x 128 fp32 matrix per (slot, v-head), each in the order its reader
+// wants, so that every copy reads whole lines:
+// * S_in(1) and R_s: register image of the scan's state layout, 16-byte unit
+//   (8 (row / 16) + t) 64 + lane holds row 16 (row / 16) + lane % 16, columns
+//   32 (t / 2) + 8 (lane / 16) + 4 (t % 2) + 0..3;
+// * M_s: LDS image of M_s^T split into bf16 hi units (0 .. 2047) then lo units; unit
+//   16 j + (cu ^ kswz(j)) holds M_s[8 cu .. 8 cu + 7][j].
+constexpr int64_t kSlotFloats = 128 * 128;
+constexpr int kMtUnits = 2048;
+constexpr int kSegMinChunks = 4;            // shortest segment (before balancing)
+// Segment lengths balance the two passes (measured on MI355X): a segment-0 chunk, which
+// writes outputs in pass A, costs ~1/0.83 of a state-map chunk, and each chain step
+// delays a pass-C segment by ~0.9 chunk-times, so segment s >= 1 gets 0.9 (s - 1) chunks
+// fewer than segment 1.
+constexpr float kSegFirstWeight = 0.83f;
+constexpr float kSegChainChunks = 0.9f;
+
+// ------------------------------------------------------------------------- plan
+struct PlanArgs {
+    const void *cu;
+    int cu64, N, T, HO, nc;  // nc: chunk-table capacity (workspace bound)
+    int32_t *header, *chunk_tok0, *chunk_len, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
+    bf16_t *out;
+    int64_t o_st, o_sh;
+    // segments (seg_G >= 3): at most seg_G segments per sequence; job entries of 8 ints
+    // {sequence, kind, first chunk, end chunk, slot, chain steps, last}, pass A from
+    // jobs[0], pass C from jobs[8 seg_capA]; counts in header[1], header[2]
+    int seg_G, seg_capA;
+    int32_t *jobs;
+};
+
+constexpr int kPlanSortMax = 512;
+
+// ------------------------------------------------------------------------- LDS copies
+#define GDN_LDS __attribute__((address_space(3)))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i writes
+// dst + 16 i; dst is wave-uniform, src is per lane.
+__device__ __forceinline__ void dma16(const char *src, void *dst)
+{
+    __builtin_amdgcn_global_load_lds((const void *)src, (GDN_LDS void *)dst, 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane n receives element n % 4 of the
+// four 8-byte pieces addressed by lanes n / 4 + 4 r, r = 0..3 (element r of the result).
+__device__ __forceinline__ u32x2 lds_tr16(const void *p)
+{
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GDN_LDS s16x4 *)p);
+    return __builtin_bit_cast(u32x2, r);
+}
+
+// Wait for this wave's LDS copies, then for the whole workgroup.
+__device__ __forceinline__ void dma_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    lds_barrier();
+}
+
+// ------------------------------------------------------------------------- prep
+struct PrepArgs {
+    const bf16_t *q, *k, *a, *b;
+    const float *A_log, *dt_bias;
+    // element strides, host-checked to fit 31 bits (32-bit here keeps scalar registers free)
+    int32_t q_st, q_sh, k_st, k_sh, a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
+    const int32_t *header, *chunk_tok0, *chunk_len;
+    char *records;
+    int HQK, HV, ratio;
+    float scale;
+};
+
+// ------------------------------------------------------------------------- scan
+struct ScanArgs {
+    const bf16_t *q, *k, *v;
+    const float *state;
+    float *new_state;
+    bf16_t *out;
+    int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
+    int64_t st_sn, st_sh, st_sv, ns_sn, ns_sh, ns_sv;
+    const int32_t *header, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
+    const char *records;
+    int HQK, HV, ratio, ngroups;
+    // Segment jobs (jobs != nullptr): the grid walks entries jobs[8 (job_first + e)] =
+    // {sequence, kind, first chunk, end chunk, slot, chain steps, last} for
+    // e < header[njob_idx] instead of whole sequences. Slot buffers hold one 128 x 128
+    // fp32 matrix per (slot, v-head): S_in(1) (seg_sin), R_s (seg_r), or M_s as bf16 hi /
+    // lo units (seg_mt, kMtUnits).
+    const int32_t *jobs;
+    int job_first, njob_idx;
+    float *seg_sin, *seg_r, *seg_mt;
+};
+
+
+// LDS layouts (16-byte units). A ds_read_b128 is served in four cycles of 16 lanes: the
+// lanes of one 32-lane half whose lane bits 2, 3, 4 have equal parity; a cycle is
+// conflict-free when its 16 lanes touch 16 distinct units modulo 256 bytes (measured on
+// gfx950). Every b128 operand read below meets that:
+//   K row t, k-chunk c (k = 8c .. 8c+7)   -> unit 16 t + (c ^ kswz(t))
+//   Q row t, k-chunk c                    -> unit 16 t + (c ^ (t & 15))
+//   V row t, v-chunk c                    -> unit 2 NW t + (c ^ 2 (t & 3))
+//   T' row r, column chunk c (8 columns)  -> unit tlay(r, c)
+//   P' row r, column chunk c              -> unit play(r, c)
+// T' is read with rows in the permuted order of the X / U tiles, P' in token order; both
+// layouts are bit permutations of (r, c) that put a read's four free lane bits into the
+// low unit bits and its tile / k-step into high ones (additive offsets).
+__host__ __device__ constexpr int kswz(int t)
+{
+    return ((t & 1) ? 1 : 0) ^ ((t & 2) ? 14 : 0) ^ ((t & 8) ? 6 : 0) ^ ((t & 16) ? 4 : 0);
+}
+__host__ __device__ constexpr int tlay(int r, int c)
+{
+    return (r & 3) | (((r >> 3) & 1) << 2) | ((c & 1) << 3) | (((r >> 4) & 1) << 4) |
+           (((c >> 1) & 1) << 5) | ((c >> 2) << 6) | (((r >> 2) & 1) << 7) | ((r >> 5) << 8);
+}
+__host__ __device__ constexpr int play(int r, int c)
+{
+    return (r & 7) | ((c & 1) << 3) | (((r >> 3) & 1) << 4) | (((c >> 1) & 1) << 5) |
+           ((c >> 2) << 6) | (((r >> 4) & 1) << 7) | ((r >> 5) << 8);
+}
+// Inverses (unit -> row, column chunk), used by the record copies.
+__host__ __device__ constexpr int tlay_row(int u)
+{
+    return (u & 3) | (((u >> 7) & 1) << 2) | (((u >> 2) & 1) << 3) | (((u >> 4) & 1) << 4) |
+           ((u >> 8) << 5);
+}
+__host__ __device__ constexpr int play_row(int u)
+{
+    return (u & 7) | (((u >> 4) & 1) << 3) | (((u >> 7) & 1) << 4) | ((u >> 8) << 5);
+}
+__host__ __device__ constexpr int lay_col(int u)
+{
+    return ((u >> 3) & 1) | (((u >> 5) & 1) << 1) | (((u >> 6) & 1) << 2);
+}
+constexpr bool layouts_invert()
+{
+    for (int r = 0; r < 64; ++r)
+        for (int c = 0; c < 8; ++c)
+            if (tlay_row(tlay(r, c)) != r || lay_col(tlay(r, c)) != c ||
+                play_row(play(r, c)) != r || lay_col(play(r, c)) != c)
+                return false;
+    return true;
+}
+static_assert(layouts_invert(), "T' / P' LDS layouts must be bijections");
+
+// ------------------------------------------------------------------------- kernels
+// Defined in gdn_prefill_plan.hip, gdn_prefill_prep.hip and gdn_prefill_scan.hip; the
+// scan kernels are instantiated there for SEG = false (whole sequences) and true
+// (segment jobs).
+__global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p);
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gdn_prefill_prep1_kernel(PrepArgs p);
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void
+gdn_prefill_prep2_kernel(PrepArgs p);
+template <bool SEG>
+__global__ __launch_bounds__(512) void gdn_prefill_scan8_kernel(ScanArgs p);
+template <bool SEG>
+__global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p);
+
+}  // namespace gdn

@@ -1,0 +1,192 @@
+// Prefill plan kernel: sequence -> chunk tables from cu_seqlens on the device, longest-
+// first sequence order, segment job tables, zero-fill of rows outside every sequence.
+#include "gdn_prefill.h"
+
+namespace gdn {
+
+__global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
+{
+    const int tid = threadIdx.x;
+    if (blockIdx.x == 0) {
+        // Chunk counts are clamped so that malformed (non-monotone) cu_seqlens can
+        // never index past the chunk tables or records sized for nc chunks; for
+        // valid input sum(ceil(len / C)) <= ceil(T / C) + N = nc always holds.
+        __shared__ int64_t scan[256];
+        __shared__ int32_t s_nck[kPlanSortMax];
+        // up to kPlanSortMax sequences the chunk table is filled chunk-parallel from these
+        __shared__ int32_t s_first[kPlanSortMax], s_end[kPlanSortMax], s_t0[kPlanSortMax],
+            s_len[kPlanSortMax];
+        __shared__ int64_t s_carry;
+        const bool par = p.N <= kPlanSortMax;
+        if (tid == 0)
+            s_carry = 0;
+        __syncthreads();
+        for (int base = 0; base < p.N; base += 256) {
+            const int n = base + tid;
+            int nck = 0, t0 = 0, ln = 0;
+            if (n < p.N) {
+                int64_t a = load_cu(p.cu, p.cu64, n), b = load_cu(p.cu, p.cu64, n + 1);
+                a = a < 0 ? 0 : (a > p.T ? p.T : a);  // clamp: never index outside [0, T)
+                b = b < a ? a : (b > p.T ? p.T : b);
+                t0 = (int)a;
+                ln = (int)(b - a);
+                nck = (ln + kC - 1) / kC;
+                p.seq_tok0[n] = t0;
+                p.seq_len[n] = ln;
+                if (n < kPlanSortMax)
+                    s_nck[n] = nck;
+            }
+            scan[tid] = nck;
+            __syncthreads();
+            for (int off = 1; off < 256; off <<= 1) {
+                const int64_t add = tid >= off ? scan[tid - off] : 0;
+                __syncthreads();
+                scan[tid] += add;
+                __syncthreads();
+            }
+            const int64_t first = s_carry + scan[tid] - nck;
+            if (n < p.N) {
+                p.seq_chunk0[n] = (int32_t)(first < p.nc ? first : p.nc);
+                if (par) {
+                    s_first[n] = (int32_t)(first < p.nc ? first : p.nc);
+                    s_end[n] = (int32_t)(first + nck < p.nc ? first + nck : p.nc);
+                    s_t0[n] = t0;
+                    s_len[n] = ln;
+                } else {
+                    for (int i = 0; i < nck && first + i < p.nc; ++i) {
+                        p.chunk_tok0[first + i] = t0 + i * kC;
+                        p.chunk_len[first + i] = min(kC, ln - i * kC);
+                    }
+                }
+            }
+            __syncthreads();
+            if (tid == 255)
+                s_carry += scan[255];
+            __syncthreads();
+        }
+        if (tid == 0) {
+            const int32_t total = (int32_t)(s_carry < p.nc ? s_carry : p.nc);
+            p.seq_chunk0[p.N] = total;
+            p.header[0] = total;
+        }
+        if (par) {  // chunk c belongs to the first sequence whose chunks end after c
+            __syncthreads();
+            const int total = (int)(s_carry < p.nc ? s_carry : p.nc);
+            for (int c = tid; c < total; c += 256) {
+                int lo = 0, hi = p.N - 1;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (s_end[mid] > c)
+                        hi = mid;
+                    else
+                        lo = mid + 1;
+                }
+                const int i = c - s_first[lo];
+                p.chunk_tok0[c] = s_t0[lo] + i * kC;
+                p.chunk_len[c] = min(kC, s_len[lo] - i * kC);
+            }
+        }
+        // Longest-first order (identity when N is large).
+        __shared__ int32_t s_order[kPlanSortMax];
+        if (p.N <= kPlanSortMax) {
+            for (int n = tid; n < p.N; n += 256) {
+                const int mine = s_nck[n];
+                int rank = 0;
+                for (int m = 0; m < p.N; ++m) {
+                    const int o = s_nck[m];
+                    rank += (o > mine) || (o == mine && m < n);
+                }
+                p.seq_order[rank] = n;
+                s_order[rank] = n;
+            }
+        } else {
+            for (int n = tid; n < p.N; n += 256)
+                p.seq_order[n] = n;
+        }
+        if (p.seg_G >= 3 && par) {  // segment job tables (host only asks for small N)
+            __syncthreads();
+            if (tid == 0) {
+                auto put = [&](int idx, int n, int kind, int cb, int ce, int q, int steps, int last) {
+                    int32_t *e = p.jobs + 8 * idx;
+                    e[0] = n;
+                    e[1] = kind;
+                    e[2] = cb;
+                    e[3] = ce;
+                    e[4] = q;
+                    e[5] = steps;
+                    e[6] = last;
+                };
+                // pass A: every segment 0 first (longest sequences first), then the state
+                // maps; slots q .. q + G - 2 of a sequence hold S_in(1) and M_s, R_s of the
+                // middle segments s (slot q + s - 1)
+                int na = 0, nc3 = 0;
+                for (int pass = 0; pass < 2; ++pass) {
+                    int qs = 0;
+                    for (int i = 0; i < p.N; ++i) {
+                        const int n = s_order[i];
+                        const int ncks = s_end[n] - s_first[n];
+                        int G = min(p.seg_G, max(1, ncks / kSegMinChunks));
+                        const int Ls = (ncks + G - 1) / G;
+                        G = Ls > 0 ? (ncks + Ls - 1) / Ls : 1;
+                        if (G < 3)
+                            G = 1;  // two segments would run one after the other
+                        // boundary of segment sg: balanced lengths (see kSegFirstWeight) when
+                        // every segment keeps at least 2 chunks, else equal lengths
+                        const float base = (ncks + kSegChainChunks * (G - 1) * (G - 2) / 2) /
+                                           (kSegFirstWeight + G - 1);
+                        const bool bal = G > 1 && base - kSegChainChunks * (G - 2) >= 2.f &&
+                                         kSegFirstWeight * base >= 2.f;
+                        auto bnd = [&](int sg) {
+                            if (sg >= G)
+                                return ncks;
+                            if (!bal)
+                                return min(sg * Ls, ncks);
+                            // chunks before segment sg: kSegFirstWeight base + sum over
+                            // u = 1 .. sg - 1 of (base - kSegChainChunks (u - 1))
+                            const float x = kSegFirstWeight * base + (sg - 1) * base -
+                                            kSegChainChunks * (sg - 1) * (sg - 2) / 2;
+                            return min(max((int)(x + 0.5f), sg), ncks);
+                        };
+                        const int q = G > 1 ? qs : -1;
+                        qs += G - 1;
+                        if (pass == 0) {
+                            put(na++, n, kJobFirst, 0, G > 1 ? bnd(1) : ncks, q, 0, 0);
+                            continue;
+                        }
+                        for (int sg = 1; sg < G; ++sg) {
+                            const int cb = bnd(sg), ce = bnd(sg + 1);
+                            if (sg < G - 1) {
+                                put(na++, n, kJobZero, cb, ce, q + sg - 1, 0, 0);
+                                put(na++, n, kJobIdent, cb, ce, q + sg - 1, 0, 0);
+                            }
+                            put(p.seg_capA + nc3++, n, kJobResume, cb, ce, q, sg - 1, sg == G - 1);
+                        }
+                    }
+                }
+                p.header[1] = na;
+                p.header[2] = nc3;
+            }
+        }
+        return;
+    }
+    // Zero-fill output rows of tokens outside [cu[0], cu[N]).
+    int64_t g0 = p.N > 0 ? load_cu(p.cu, p.cu64, 0) : p.T;
+    g0 = g0 < 0 ? 0 : (g0 > p.T ? p.T : g0);
+    int64_t g1 = p.N > 0 ? load_cu(p.cu, p.cu64, p.N) : p.T;
+    g1 = g1 < g0 ? g0 : (g1 > p.T ? p.T : g1);
+    const int64_t gap = g0 + (p.T - g1);
+    const int64_t vec_per_tok = (int64_t)p.HO * (kDK / 8);
+    const int64_t total = gap * vec_per_tok;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int64_t i = (int64_t)(blockIdx.x - 1) * 256 + tid; i < total;
+         i += (int64_t)(gridDim.x - 1) * 256) {
+        const int64_t gt = i / vec_per_tok;
+        const int64_t rem = i % vec_per_tok;
+        const int64_t tok = gt < g0 ? gt : g1 + (gt - g0);
+        const int64_t hh = rem / (kDK / 8);
+        const int64_t col = (rem % (kDK / 8)) * 8;
+        *(u32x4 *)(p.out + tok * p.o_st + hh * p.o_sh + col) = z;
+    }
+}
+
+}  // namespace gdn

@@ -1,0 +1,402 @@
+// Prefill prep kernels: per (chunk, q/k head, v-head pair) unit, gates, P' and
+// T' = (I + A)^-1 diag(beta) into the chunk's records.
+#include "gdn_prefill.h"
+
+namespace gdn {
+
+// Row order inside a 16-row block used for fp32 MFMA operands: pi(m) = 4 (m % 4) + m / 4
+// (a 4 x 4 transpose, its own inverse). With pi-ordered rows an MFMA result in C layout
+// (lane (n, g) holds rows 4 g + i) already holds rows 4 i + g: exactly the operand
+// layout of the next v_mfma_f32_16x16x4_f32 (k-slice i, lane (n, g) supplies k = 4 i + g).
+__device__ __forceinline__ int pi16(int m) { return 4 * (m & 3) + (m >> 2); }
+
+// acc += coef * (acc of lane K in this 16-lane row): one v_fmac_f32 with a DPP row_newbcast
+// source. Callers keep >= 2 other VALU instructions between the last write of acc and
+// this read (the DPP read-after-write hazard); the first use in a chain is preceded by
+// s_nop 1.
+#define GDN_FMAC_BCAST(acc, coef, K)                                                     \
+    asm volatile("v_fmac_f32_dpp %0, %0, %1 row_newbcast:" #K " row_mask:0xf bank_mask:0xf" \
+                 : "+v"(acc)                                                              \
+                 : "v"(coef))
+
+// Work unit: (chunk, q/k head, group of VH v-heads). A persistent workgroup of 4 VH waves
+// walks units u = blockIdx.x, + gridDim.x, ...; wave (hv, w) = v-head hv of the group,
+// block w. The unit's K and Q go to LDS once (direct copies; K double-buffered, the next
+// unit's copies and gate inputs in flight while this one computes) and serve every
+// v-head of the group. Per unit, wave (hv, w):
+//   * writes P' row block w: P'[t, j] = scale 2^(L_t - L_j) q_t . k_j, j <= t;
+//   * forms A column block w, A[t, j] = beta_t 2^(L_t - L_j) k_t . k_j (j < t): the
+//     diagonal block stays in registers, blocks (i > w, w) go to LDS for every wave;
+//   * inverts X_w = (I + A_ww)^-1 by forward substitution (DPP broadcasts);
+//   * after a barrier (all X_i and A blocks published): column block w of T = (I + A)^-1,
+//       T_ww = X_w,  T_iw = -X_i sum_{m=w}^{i-1} A_im T_mw  (i > w),
+//     on fp32 MFMA with every operand in registers, and writes T' = T diag(beta);
+// wave (hv, 3), which has the least work after the barrier, also computes the next unit's
+// gates and cumulative log2 decay L.
+// (gdn_prefill/solution/triton/kernel.py:60-79 form the same A, T and P.)
+template <int VH>
+struct PrepSmem {
+    u32x4 K[2][kC * 16];  // row t, k-chunk c at unit 16 t + (c ^ (t & 15))
+    u32x4 Q[kC * 16];
+    float L[2][VH][64];   // L by token
+    float LT[2][VH][64];  // L of token 16 b + 4 i + g at 16 b + 4 g + i
+    float B[2][VH][64];   // beta by token
+    u32x4 XA[VH][4][64];  // X_w in A-operand layout, by lane, split4
+    u32x4 AO[VH][6][64];  // off-diagonal A_im (m < i) as XA; index i(i-1)/2 + m
+    float Ms[4 * VH][16][16];  // per wave: -A_ww rows, X_w, then T' staging
+};
+
+constexpr int kGateWave = 3;  // column block with no work after the barrier
+
+template <int VH>
+__device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
+{
+    const int ngrp = p.ratio / VH;
+    const int nunits = p.header[0] * p.HQK * ngrp;
+    // wv is wave-uniform: branches on the column block are scalar branches
+    const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
+              lr = l & 15, lg = l >> 4;
+    // Waves are dealt to the 4 SIMDs round-robin: the second v-head takes the blocks in
+    // reverse, so each SIMD pairs a heavy column block (w = 0) with a light one.
+    const int hv = wv >> 2, w = hv & 1 ? 3 - (wv & 3) : (wv & 3);
+    const uint32_t kst2 = (uint32_t)p.k_st * 2, qst2 = (uint32_t)p.q_st * 2;
+
+    struct Unit {
+        int c, g, h, tok0, len;
+    };
+    auto unit = [&](int u) {
+        Unit r;
+        const int grp = u / ngrp, hg = u % ngrp;
+        r.c = grp / p.HQK;
+        r.g = grp % p.HQK;
+        r.h = r.g * p.ratio + hg * VH + hv;
+        r.tok0 = p.chunk_tok0[r.c];
+        r.len = p.chunk_len[r.c];
+        return r;
+    };
+    // K or Q of a unit -> LDS: 16 windows of 64 16-byte units (4 rows each) per matrix,
+    // dealt to the waves. Rows past the chunk's end repeat its last token: they meet
+    // beta = 0 or the causal mask only.
+    auto copy = [&](const Unit &U, bool isq, u32x4 *dst) {
+        const char *base = isq ? (const char *)(p.q + (int64_t)U.tok0 * p.q_st + (int64_t)U.g * p.q_sh)
+                               : (const char *)(p.k + (int64_t)U.tok0 * p.k_st + (int64_t)U.g * p.k_sh);
+        const uint32_t st2 = isq ? qst2 : kst2;
+#pragma unroll
+        for (int i = 0; i < 4 / VH; ++i) {
+            const int b = wv + 4 * VH * i;
+            const int t = 4 * b + (l >> 4), cs = l & 15;
+            dma16(base + (uint32_t)min(t, U.len - 1) * st2 + 16u * (cs ^ (t & 15)), &dst[64 * b]);
+        }
+    };
+    // Gates (gdn_decode/solution/triton/kernel.py:128-131); padding tokens: alpha = 1,
+    // beta = 0. Cumulative decay in log2 units: every factor below is 2^(non-positive
+    // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow).
+    // The raw bf16 bits are kept until gates() converts them at the end of the unit: a
+    // conversion here would make the gate wave wait for these loads at the unit's start.
+    auto gate_in = [&](const Unit &U, uint32_t &a_in, uint32_t &b_in) {
+        const int tl = U.tok0 + min(l, U.len - 1);
+        a_in = p.a[(int64_t)tl * p.a_st + (int64_t)U.h * p.a_sh];
+        b_in = p.b[(int64_t)tl * p.b_st + (int64_t)U.h * p.b_sh];
+    };
+    auto gates = [&](const Unit &U, uint32_t a_raw, uint32_t b_raw, int buf) {
+        const float a_in = bf16_to_f32(a_raw), b_in = bf16_to_f32(b_raw);
+        // log2 alpha = -exp(A_log) log2(1 + e^x) (x > 20: -exp(A_log) x log2 e), with the
+        // hardware base-2 exp / log; beta = 1 / (1 + e^-b)
+        constexpr float kLog2e = 1.44269504088896340736f;
+        float L = 0.f, bt = 0.f;
+        if (l < U.len) {
+            const float x = a_in + p.dt_bias[(int64_t)U.h * p.dt_s];
+            const float sp2 = x > 20.f ? x * kLog2e
+                                       : __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(x * kLog2e));
+            L = -expf(p.A_log[(int64_t)U.h * p.A_log_s]) * sp2;
+            bt = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-b_in * kLog2e));
+        }
+        L = wave_prefix_sum(L);  // cumulative log2 decay
+        const float Lend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 63));
+        sm.L[buf][hv][l] = L;
+        sm.B[buf][hv][l] = bt;
+        sm.LT[buf][hv][16 * (l >> 4) + 4 * (l & 3) + ((l >> 2) & 3)] = L;
+        char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
+        float *gts = (float *)(rec + kRecGates);
+        const float gam = __builtin_amdgcn_exp2f(L);
+        gts[l] = gam;
+        gts[64 + l] = __builtin_amdgcn_exp2f(Lend - L);
+        gts[128 + l] = p.scale * gam;
+        if (l == 0)
+            gts[192] = __builtin_amdgcn_exp2f(Lend);
+        if (l < 4)
+            ((float *)(rec + kRecZero))[l] = 0.f;
+    };
+
+    // MFMA operand: 16 rows, k-chunk 4 ks + lg.
+    auto kop = [&](const u32x4 *M, int row, int ks) {
+        return M[16 * row + ((4 * ks + lg) ^ (row & 15))];
+    };
+    float (*Ms)[16] = sm.Ms[wv];
+
+    // Diagonal-block masks of this lane, one bit per element: bits 0..3 keep P'[t][j] for
+    // j <= t (t = 16 w + lr, j = 16 w + 4 lg + e), bits 4..7 keep A[t][j] for j < t
+    // (t = 16 w + pi(lr), j = 16 w + 4 e + lg). They do not depend on w.
+    int dbits0 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        dbits0 |= (4 * lg + e <= lr) << e;
+        dbits0 |= (4 * e + lg < pi16(lr)) << (4 + e);
+    }
+    auto compute = [&](const Unit &U, const u32x4 *Kb, int buf, uint32_t &na, uint32_t &nb,
+                       const Unit &N, bool more) {
+        char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
+        const float *Ls = sm.L[buf][hv], *Bs = sm.B[buf][hv], *LsT = sm.LT[buf][hv];
+        // re-derived per unit, so the compiler keeps one register instead of hoisting a
+        // lane mask per element out of the unit loop (they spilled to VGPR lanes)
+        int dbits = dbits0;
+        asm volatile("" : "+v"(dbits));
+
+        // P' row block w: lane (t = 16 w + lr, lg) holds columns 16 jb + 4 lg .. +3. All
+        // blocks' MFMAs issue before any scaling / store, which then never waits on them.
+        {
+            const int t = 16 * w + lr;
+            const float Lt = Ls[t];
+            u32x4 qn[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                qn[ks] = kop(sm.Q, t, ks);
+            f32x4 rp[4];
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                if (jb > w)
+                    break;
+                rp[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    rp[jb] = mfma_bf16(kop(Kb, 16 * jb + lr, ks), qn[ks], rp[jb]);
+            }
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+                if (jb > w)
+                    break;
+                const f32x4 Lj = *(const f32x4 *)&Ls[16 * jb + 4 * lg];
+                float pv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    pv[e] = p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * rp[jb][e];
+                if (jb == w) {  // diagonal block: zero above the diagonal
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        pv[e] = keep_if(pv[e], dbits, e);
+                }
+                *(u32x2 *)(rec + kRecP + 2 * (tri_blk(w, jb) * kBlk + lr * 16 + 4 * lg)) =
+                    u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+            }
+        }
+
+        // A column block w: lane (lr, lg) element e = A[16 i + pi(lr)][16 w + 4 e + lg],
+        // blocks i = w .. 3; MFMAs first, then scaling.
+        f32x4 Aww = {0.f, 0.f, 0.f, 0.f};
+        {
+            u32x4 kw[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                kw[ks] = kop(Kb, 16 * w + pi16(lr), ks);
+            f32x4 ra[4];
+#pragma unroll
+            for (int i = 3; i >= 0; --i) {
+                if (i < w)
+                    break;
+                ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+                    ra[i] = mfma_bf16(kw[ks], kop(Kb, 16 * i + pi16(lr), ks), ra[i]);
+            }
+            const f32x4 Lm = *(const f32x4 *)&LsT[16 * w + 4 * lg];
+#pragma unroll
+            for (int i = 3; i >= 0; --i) {
+                if (i < w)
+                    break;
+                const int t = 16 * i + pi16(lr);
+                const float Lt = Ls[t], btt = Bs[t];
+                f32x4 av;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    av[e] = btt * __builtin_amdgcn_exp2f(Lt - Lm[e]) * ra[i][e];
+                if (i == w) {  // diagonal block: strictly lower part only
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        av[e] = keep_if(av[e], dbits, 4 + e);
+                    Aww = av;
+                } else
+                    sm.AO[hv][i * (i - 1) / 2 + w][l] = split4(av);
+            }
+        }
+
+        // X_w = (I + A_ww)^-1. Lane (lr, lg) holds row pi(lr), columns lg + 4 s (s = 0..3)
+        // of X; step m subtracts A[r][m] x (row m of X), row m being final (A is strictly
+        // lower, so rows r <= m see A[r][m] = 0). Row m sits in lane pi(m) of every 16-lane
+        // row, next to the same columns.
+        f32x4 xw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            Ms[pi16(lr)][4 * e + lg] = -Aww[e];
+        {
+            float arow[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = *(const f32x4 *)&Ms[pi16(lr)][4 * q];
+                arow[4 * q] = v[0]; arow[4 * q + 1] = v[1]; arow[4 * q + 2] = v[2]; arow[4 * q + 3] = v[3];
+            }
+            float x[4];
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+                x[s2] = pi16(lr) == lg + 4 * s2 ? 1.f : 0.f;
+            asm volatile("s_nop 1" ::: "memory");
+            // arow holds -A; the broadcast lane of step M is pi(M)
+#define GDN_SUBST_STEP(M, K)                                                      \
+            GDN_FMAC_BCAST(x[0], arow[M], K); GDN_FMAC_BCAST(x[1], arow[M], K);   \
+            GDN_FMAC_BCAST(x[2], arow[M], K); GDN_FMAC_BCAST(x[3], arow[M], K);
+            GDN_SUBST_STEP(0, 0) GDN_SUBST_STEP(1, 4) GDN_SUBST_STEP(2, 8) GDN_SUBST_STEP(3, 12)
+            GDN_SUBST_STEP(4, 1) GDN_SUBST_STEP(5, 5) GDN_SUBST_STEP(6, 9) GDN_SUBST_STEP(7, 13)
+            GDN_SUBST_STEP(8, 2) GDN_SUBST_STEP(9, 6) GDN_SUBST_STEP(10, 10) GDN_SUBST_STEP(11, 14)
+            GDN_SUBST_STEP(12, 3) GDN_SUBST_STEP(13, 7) GDN_SUBST_STEP(14, 11)
+#undef GDN_SUBST_STEP
+            xw = f32x4{x[0], x[1], x[2], x[3]};
+        }
+        sm.XA[hv][w][l] = split4(xw);
+        // X_w in B-operand layout (lane (n, lg) element s = X[4 s + lg][n]) via the scratch
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            Ms[pi16(lr)][lg + 4 * s2] = xw[s2];
+        f32x4 TB[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+            TB[0][s2] = Ms[4 * s2 + lg][lr];
+        // every X_i is in XA, every A_im in AO; every wave is done with Q (the next unit's K
+        // copy stays in flight)
+        lds_barrier_inflight();
+        if (more)
+            copy(N, true, sm.Q);
+
+        // Column block w of T; TB[i] = T_(w+i),w in B-operand layout.
+        // T_iw = -X_i z, z = sum_m A_im T_mw, with every 16x16x16 block product split into
+        // bf16 hi / lo terms a_h b_h + a_l b_h + a_h b_l (a_l b_l, ~2^-16 relative, dropped).
+        // An MFMA only pairs lane (m, g)'s k-slot j of A with lane (n, g)'s k-slot j of B, so
+        // the fp32 operand layouts carry over (slot j = column 4 j + g), and a 16x16x32 MFMA
+        // with A = [a_h | a_l], B = [b_h | b_h] computes two terms: column 0 takes 16 bf16
+        // MFMAs instead of 36 fp32 ones at twice their cost.
+        u32x4 TS[4];
+        TS[0] = split4(TB[0]);
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            if (i + w > 3)
+                break;
+            u32x4 as[3];
+#pragma unroll
+            for (int m = 0; m < i; ++m) {  // A block (i + w, m + w)
+                const int ii = i + w, mm = m + w;
+                as[m] = sm.AO[hv][ii * (ii - 1) / 2 + mm][l];
+            }
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < i; ++m)
+                z = mfma_bf16(as[m], u32x4{TS[m][0], TS[m][1], TS[m][0], TS[m][1]}, z);
+#pragma unroll
+            for (int m = 0; m < i; m += 2) {
+                if (m + 1 < i)
+                    z = mfma_bf16(u32x4{as[m][0], as[m][1], as[m + 1][0], as[m + 1][1]},
+                                  u32x4{TS[m][2], TS[m][3], TS[m + 1][2], TS[m + 1][3]}, z);
+                else
+                    z = mfma_bf16_k16(u32x2{as[m][0], as[m][1]}, u32x2{TS[m][2], TS[m][3]}, z);
+            }
+            const u32x4 xs = sm.XA[hv][i + w][l];
+            const u32x4 zs = split4(z);
+            f32x4 t = mfma_bf16(xs, u32x4{zs[0], zs[1], zs[0], zs[1]}, f32x4{0.f, 0.f, 0.f, 0.f});
+            t = mfma_bf16_k16(u32x2{xs[0], xs[1]}, u32x2{zs[2], zs[3]}, t);
+            TB[i] = -t;
+            if (i + w < 3)
+                TS[i] = split4(TB[i]);
+        }
+
+        // T' = T diag(beta) -> record (bf16 hi / lo, block layout), one block at a time
+        // through this wave's fp32 staging tile: lane (row l / 4, columns 4 (l % 4) .. +3)
+        // splits its four values and stores 8 bytes of hi and 8 of lo.
+        const float bcol = Bs[16 * w + lr];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i + w > 3)
+                break;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2)
+                Ms[4 * s2 + lg][lr] = TB[i][s2] * bcol;
+            const f32x4 v = *(const f32x4 *)&Ms[l >> 2][4 * (l & 3)];
+            uint32_t h01, l01, h23, l23;
+            split_bf16x2(v[0], v[1], h01, l01);
+            split_bf16x2(v[2], v[3], h23, l23);
+            const int off = tri_blk(i + w, w) * 512 + (l >> 2) * 32 + 8 * (l & 3);
+            *(u32x2 *)(rec + kRecThi + off) = u32x2{h01, h23};
+            *(u32x2 *)(rec + kRecTlo + off) = u32x2{l01, l23};
+        }
+
+        // next unit's gates (its inputs were loaded one unit ago)
+        if (more && w == kGateWave)
+            gates(N, na, nb, buf ^ 1);
+    };
+
+    int u = blockIdx.x;
+    if (u >= nunits)
+        return;
+    Unit U = unit(u);
+    uint32_t a_in = 0, b_in = 0;
+    copy(U, false, sm.K[0]);
+    copy(U, true, sm.Q);
+    if (w == kGateWave) {
+        gate_in(U, a_in, b_in);
+        gates(U, a_in, b_in, 0);
+    }
+    for (;;) {
+        // even step: K in sm.K[0], gates in buffer 0
+        int un = u + gridDim.x;
+        bool more = un < nunits;
+        Unit N = more ? unit(un) : U;
+        dma_barrier();
+        if (more) {
+            copy(N, false, sm.K[1]);
+            if (w == kGateWave)
+                gate_in(N, a_in, b_in);
+        }
+        compute(U, sm.K[0], 0, a_in, b_in, N, more);
+        if (!more)
+            break;
+        u = un;
+        U = N;
+        // odd step: K in sm.K[1], gates in buffer 1
+        un = u + gridDim.x;
+        more = un < nunits;
+        N = more ? unit(un) : U;
+        dma_barrier();
+        if (more) {
+            copy(N, false, sm.K[0]);
+            if (w == kGateWave)
+                gate_in(N, a_in, b_in);
+        }
+        compute(U, sm.K[1], 1, a_in, b_in, N, more);
+        if (!more)
+            break;
+        u = un;
+        U = N;
+    }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+gdn_prefill_prep1_kernel(PrepArgs p)
+{
+    __shared__ PrepSmem<1> sm;
+    prep_body<1>(p, sm);
+}
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void
+gdn_prefill_prep2_kernel(PrepArgs p)
+{
+    __shared__ PrepSmem<2> sm;
+    prep_body<2>(p, sm);
+}
+
+}  // namespace gdn

@@ -20,7 +20,9 @@ def test_pack_metadata(name, entry):
     assert doc["spec"]["entry_point"] == entry
     assert doc["spec"]["destination_passing_style"] is True
     paths = {s["path"] for s in doc["sources"]}
-    assert {"kernel.py", "gdn_hip/api.py", "csrc/gdn_prefill.hip", "include/gdn_hip.h"} <= paths
+    assert {"kernel.py", "gdn_hip/api.py", "csrc/gdn_prefill.hip", "csrc/gdn_prefill.h",
+            "csrc/gdn_prefill_plan.hip", "csrc/gdn_prefill_prep.hip", "csrc/gdn_prefill_scan.hip",
+            "include/gdn_hip.h"} <= paths
     assert not any(p.startswith("oracle") for p in paths)  # the checker never ships
     json.dumps(doc)
 
