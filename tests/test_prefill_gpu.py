@@ -231,6 +231,18 @@ def test_prefill_segments_mixed(dev, lens, hqk, hv):
                              state_std=0.05), f"segments lens={lens}")
 
 
+def test_prefill_segments_inplace_state(dev):
+    """Segmented scan with new_state aliasing state: pass A reads the initial state only in
+    segment 0's job, and only the last segment's pass-C job writes the final state."""
+    inp = prefill_inputs([2048, 1100], seed=53, with_state=True, gates="mild", state_std=0.05)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out, ns = gdn_prefill(*g.args(), new_state=g.state)
+    torch.cuda.synchronize()
+    assert ns.data_ptr() == g.state.data_ptr()
+    _check(out, ns, ref_out, ref_ns, "segments in-place")
+
+
 def test_prefill_segments_match_whole_sequence_scan(dev):
     """The segmented scan and the whole-sequence scan (tuning variant 2) agree."""
     from gdn_hip.api import set_prefill_variant
