@@ -78,6 +78,8 @@ constexpr int kRecThi = 0;       // bf16 [10][16][16]  T' = (I + A)^-1 diag(beta
 constexpr int kRecTlo = 5120;    // bf16 [10][16][16]  low half
 constexpr int kRecP = 10240;     // bf16 [10][16][16]  P' = scale * P (decayed, causal Q K^T)
 constexpr int kRecGates = 15360; // f32 gamma[64], dec[64], scale * gamma[64], gammaC
+// T', P' and dec are held up to a diagonal similarity diag(2^lo) that carries the low part
+// of the cumulative log decay (gdn_prefill_prep.hip, gates); the scan uses them as they are.
 constexpr int kRecZero = 16256;  // 16 zero bytes (after the gates): what absent blocks read
 constexpr int kRecBytes = 16384;
 
@@ -112,18 +114,33 @@ __device__ __forceinline__ float dpp_or0(float x)
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xF, true));
 }
 
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_or0_f64(double x)
+{
+    const int64_t v = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true),
+              hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, ROWS, 0xF, true);
+    return __longlong_as_double((int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
 // Inclusive prefix sum over the 64 lanes: shifts by 1, 2, 4, 8 inside each 16-lane row,
 // then row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then the total of
-// rows 0-1 into rows 2-3 (row_bcast:31).
-__device__ __forceinline__ float wave_prefix_sum(float x)
+// rows 0-1 into rows 2-3 (row_bcast:31). Carried in fp64 (v_add_f64 is full rate) and
+// returned as an unevaluated pair hi + lo of floats, hi the correctly rounded sum: lanes
+// combine different partial sums, so single-float prefix sums of large values differ by an
+// ulp where the exact sums are equal, while the pair keeps every difference of two lanes'
+// sums to ~2^-48 of their size.
+__device__ __forceinline__ void wave_prefix_sum_pair(float x, float &hi, float &lo)
 {
-    x += dpp_or0<0x111, 0xF>(x);
-    x += dpp_or0<0x112, 0xF>(x);
-    x += dpp_or0<0x114, 0xF>(x);
-    x += dpp_or0<0x118, 0xF>(x);
-    x += dpp_or0<0x142, 0xA>(x);
-    x += dpp_or0<0x143, 0xC>(x);
-    return x;
+    double s = x;
+    s += dpp_or0_f64<0x111, 0xF>(s);
+    s += dpp_or0_f64<0x112, 0xF>(s);
+    s += dpp_or0_f64<0x114, 0xF>(s);
+    s += dpp_or0_f64<0x118, 0xF>(s);
+    s += dpp_or0_f64<0x142, 0xA>(s);
+    s += dpp_or0_f64<0x143, 0xC>(s);
+    hi = (float)s;
+    lo = (float)(s - (double)hi);
 }
 
 template <int K>

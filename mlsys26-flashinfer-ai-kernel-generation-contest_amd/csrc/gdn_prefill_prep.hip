@@ -31,6 +31,7 @@ __device__ __forceinline__ int pi16(int m) { return 4 * (m & 3) + (m >> 2); }
 //   * after a barrier (all X_i and A blocks published): column block w of T = (I + A)^-1,
 //       T_ww = X_w,  T_iw = -X_i sum_{m=w}^{i-1} A_im T_mw  (i > w),
 //     on fp32 MFMA with every operand in registers, and writes T' = T diag(beta);
+// (T', P' and dec are stored in the similarity form given with the gates below)
 // wave (hv, 3), which has the least work after the barrier, also computes the next unit's
 // gates and cumulative log2 decay L.
 // (gdn_prefill/solution/triton/kernel.py:60-79 form the same A, T and P.)
@@ -38,8 +39,8 @@ template <int VH>
 struct PrepSmem {
     u32x4 K[2][kC * 16];  // row t, k-chunk c at unit 16 t + (c ^ (t & 15))
     u32x4 Q[kC * 16];
-    float L[2][VH][64];   // L by token
-    float LT[2][VH][64];  // L of token 16 b + 4 i + g at 16 b + 4 g + i
+    float L[2][VH][64];    // L by token: L = L_hi + L_lo (float-float), L_hi here
+    float Llo[2][VH][64];  // L_lo by token
     float B[2][VH][64];   // beta by token
     u32x4 XA[VH][4][64];  // X_w in A-operand layout, by lane, split4
     u32x4 AO[VH][6][64];  // off-diagonal A_im (m < i) as XA; index i(i-1)/2 + m
@@ -91,6 +92,16 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     // Gates (gdn_decode/solution/triton/kernel.py:128-131); padding tokens: alpha = 1,
     // beta = 0. Cumulative decay in log2 units: every factor below is 2^(non-positive
     // difference), one v_exp_f32 (results below 2^-126 flush to 0, i.e. underflow).
+    // L is summed in fp64 and kept as a float pair hi + lo: with strong decays |L| reaches
+    // 10^4..10^5 in a chunk, where one ulp of a single float is already a 0.3% error in a
+    // factor 2^(L_t - L_j) of two tokens close to each other. The lo parts never enter the
+    // 64x64 matrices: 2^(L_t - L_j) = 2^lo_t 2^(hi_t - hi_j) 2^-lo_j is a diagonal
+    // similarity, I + A = D (I + A~) D^-1 with D = diag(2^lo) and A~ built from hi alone,
+    // so T = D T~ D^-1 and U = D U~ with U~ = T~ diag(beta 2^-lo) R. Hence the record holds
+    //   T'~ = T~ diag(beta_j 2^-lo_j),  P'~[t, j] = scale 2^lo_t 2^(hi_t - hi_j) q_t . k_j,
+    //   dec~_j = 2^(L_C - L_j) 2^lo_j = 2^((hi_C - hi_j) + lo_C),
+    // and the scan's O = scale gamma (Q S0^T) + P'~ U~ and S_C = gamma_C S0 + (dec~ U~)^T K
+    // are unchanged. hi_t - hi_j is exact (Sterbenz) wherever the factor is not negligible.
     // The raw bf16 bits are kept until gates() converts them at the end of the unit: a
     // conversion here would make the gate wave wait for these loads at the unit's start.
     auto gate_in = [&](const Unit &U, uint32_t &a_in, uint32_t &b_in) {
@@ -111,16 +122,19 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
             L = -expf(p.A_log[(int64_t)U.h * p.A_log_s]) * sp2;
             bt = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-b_in * kLog2e));
         }
-        L = wave_prefix_sum(L);  // cumulative log2 decay
-        const float Lend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 63));
+        float Ll;
+        wave_prefix_sum_pair(L, L, Ll);  // cumulative log2 decay
+        const float Lend = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L), 63)),
+                    Lendl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Ll), 63));
         sm.L[buf][hv][l] = L;
+        sm.Llo[buf][hv][l] = Ll;
         sm.B[buf][hv][l] = bt;
-        sm.LT[buf][hv][16 * (l >> 4) + 4 * (l & 3) + ((l >> 2) & 3)] = L;
         char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
         float *gts = (float *)(rec + kRecGates);
+        // 2^hi alone: its error is 2^-24 |L| relative, only above 2^-24 once 2^L < 2^-126
         const float gam = __builtin_amdgcn_exp2f(L);
         gts[l] = gam;
-        gts[64 + l] = __builtin_amdgcn_exp2f(Lend - L);
+        gts[64 + l] = __builtin_amdgcn_exp2f((Lend - L) + Lendl);
         gts[128 + l] = p.scale * gam;
         if (l == 0)
             gts[192] = __builtin_amdgcn_exp2f(Lend);
@@ -146,7 +160,9 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     auto compute = [&](const Unit &U, const u32x4 *Kb, int buf, uint32_t &na, uint32_t &nb,
                        const Unit &N, bool more) {
         char *rec = p.records + ((int64_t)U.c * p.HV + U.h) * kRecBytes;
-        const float *Ls = sm.L[buf][hv], *Bs = sm.B[buf][hv], *LsT = sm.LT[buf][hv];
+        const float *Ls = sm.L[buf][hv], *Bs = sm.B[buf][hv];
+        // token 16 w + lr: its row of P'~ and its column of T'~ carry 2^+-lo
+        const float lo_w = sm.Llo[buf][hv][16 * w + lr];
         // re-derived per unit, so the compiler keeps one register instead of hoisting a
         // lane mask per element out of the unit loop (they spilled to VGPR lanes)
         int dbits = dbits0;
@@ -156,7 +172,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         // blocks' MFMAs issue before any scaling / store, which then never waits on them.
         {
             const int t = 16 * w + lr;
-            const float Lt = Ls[t];
+            const float Lt = Ls[t], sct = p.scale * __builtin_amdgcn_exp2f(lo_w);
             u32x4 qn[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
@@ -179,7 +195,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 float pv[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    pv[e] = p.scale * __builtin_amdgcn_exp2f(Lt - Lj[e]) * rp[jb][e];
+                    pv[e] = sct * __builtin_amdgcn_exp2f(Lt - Lj[e]) * rp[jb][e];
                 if (jb == w) {  // diagonal block: zero above the diagonal
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -208,7 +224,10 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 for (int ks = 0; ks < 4; ++ks)
                     ra[i] = mfma_bf16(kw[ks], kop(Kb, 16 * i + pi16(lr), ks), ra[i]);
             }
-            const f32x4 Lm = *(const f32x4 *)&LsT[16 * w + 4 * lg];
+            float Lm[4];  // columns 16 w + 4 e + lg
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                Lm[e] = Ls[16 * w + 4 * e + lg];
 #pragma unroll
             for (int i = 3; i >= 0; --i) {
                 if (i < w)
@@ -315,10 +334,10 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 TS[i] = split4(TB[i]);
         }
 
-        // T' = T diag(beta) -> record (bf16 hi / lo, block layout), one block at a time
+        // T'~ = T~ diag(beta 2^-lo) -> record (bf16 hi / lo, block layout), one block at a time
         // through this wave's fp32 staging tile: lane (row l / 4, columns 4 (l % 4) .. +3)
         // splits its four values and stores 8 bytes of hi and 8 of lo.
-        const float bcol = Bs[16 * w + lr];
+        const float bcol = Bs[16 * w + lr] * __builtin_amdgcn_exp2f(-lo_w);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             if (i + w > 3)

@@ -101,6 +101,25 @@ class PrefillInputs:
                              self.scale, list(self.seqlens))
 
 
+def with_extreme_gates(inp, seed=0):
+    """Copy of ``inp`` (decode or prefill inputs) whose gate inputs take extreme values:
+    a from {-30, -20.5, 19.9, 20.1, 25, 40} or N(0, 1) (both sides of softplus's x > 20
+    branch), b from {-30, -8, 0, 8, 30} (beta ~ 0 .. 1), A_log per v-head from
+    {-200, -10, 0, 2, 5} (alpha exactly 1 down to exactly 0)."""
+    g = _gen(seed)
+    a_vals = torch.tensor([-30.0, -20.5, 19.9, 20.1, 25.0, 40.0])
+    b_vals = torch.tensor([-30.0, -8.0, 0.0, 8.0, 30.0])
+    al_vals = torch.tensor([-200.0, -10.0, 0.0, 2.0, 5.0])
+    a = inp.a.float().clone()
+    pick = torch.randint(0, 8, a.shape, generator=g)
+    a = torch.where(pick < 6, a_vals[pick.clamp(max=5)], a)
+    b = b_vals[torch.randint(0, 5, inp.b.shape, generator=g)]
+    A_log = al_vals[torch.arange(inp.A_log.shape[0]) % 5].float()
+    fields = dict(inp.__dict__)
+    fields.update(a=a.to(torch.bfloat16), b=b.to(torch.bfloat16), A_log=A_log)
+    return type(inp)(**fields)
+
+
 def decode_inputs(batch, hqk=HQK, hv=HV, d=D, seed=0, with_state=True, gates="strong",
                   state_std=0.02, seq_len=1):
     g = _gen(seed)

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from gdn_hip import gdn_decode, set_decode_variant
-from gdn_hip.inputs import decode_inputs
+from gdn_hip.inputs import decode_inputs, with_extreme_gates
 from gdn_hip.parity import check_output, check_state
 from oracle import gdn_oracle as O
 
@@ -214,3 +214,16 @@ def test_decode_multi_token_in_place_and_strided(dev):
     torch.cuda.synchronize()
     assert ns.data_ptr() == g.state.data_ptr()
     _check(out, ns, ref_out, ref_ns, "T=3 in place, strided")
+
+
+@pytest.mark.parametrize("seq_len", [1, 3])
+def test_decode_extreme_gates(dev, seq_len):
+    """Gate inputs on both sides of softplus's x > 20 branch, beta ~ 0 and ~ 1, alpha
+    exactly 1 and exactly 0 (kernel.py:128-131)."""
+    inp = with_extreme_gates(decode_inputs(16, seed=61, seq_len=seq_len), seed=62)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out, ns = gdn_decode(*g.args())
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(ns).all()
+    _check(out, ns, ref_out, ref_ns, f"extreme gates T={seq_len}")

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from gdn_hip import gdn_decode, gdn_prefill
-from gdn_hip.inputs import prefill_inputs, varlen_lengths
+from gdn_hip.inputs import prefill_inputs, varlen_lengths, with_extreme_gates
 from gdn_hip.parity import check_output, check_state
 from oracle import gdn_oracle as O
 
@@ -258,3 +258,11 @@ def test_prefill_segments_match_whole_sequence_scan(dev):
     vs = check_state(ns_s, ns_w)
     print(f"[segmented vs whole] output {vo} | state {vs}", flush=True)
     assert vo.ok and vs.ok
+
+
+@pytest.mark.parametrize("lens", [[300, 77, 1000], [2048]])
+def test_prefill_extreme_gates(dev, lens):
+    """Extreme gate inputs (softplus x > 20 branch, beta ~ 0 / ~ 1, alpha exactly 1 / 0)
+    through whole-sequence and segmented scans."""
+    inp = with_extreme_gates(prefill_inputs(lens, seed=63, with_state=True), seed=64)
+    _run(dev, inp, f"extreme gates lens={lens}")
