@@ -3,6 +3,7 @@
 Tolerances (as applied here): output bf16 atol = rtol = 2e-2; new_state fp32
 rtol = 1e-3 with atol = 1e-4; both-condition rule of FAQ.md:104-110.
 """
+import numpy as np
 import pytest
 import torch
 
@@ -266,3 +267,42 @@ def test_prefill_extreme_gates(dev, lens):
     through whole-sequence and segmented scans."""
     inp = with_extreme_gates(prefill_inputs(lens, seed=63, with_state=True), seed=64)
     _run(dev, inp, f"extreme gates lens={lens}")
+
+
+def _random_case(i):
+    """Seeded random prefill case: sequence count and lengths (empty, sub-chunk, chunk
+    multiples, long), head layout, gate regime, initial state, padding tokens, cu dtype."""
+    rng = np.random.default_rng(7100 + i)
+    hqk, hv = [(16, 32), (4, 8), (8, 16), (2, 8)][i % 4]
+    n = int(rng.choice([1, 1, 2, 3, 4, 7, 12, 25]))
+    kind = rng.choice(["empty", "short", "chunk", "medium", "long"], size=n,
+                      p=[0.1, 0.2, 0.1, 0.3, 0.3])
+    lens = [int({"empty": 0, "short": rng.integers(1, 64), "chunk": 64 * rng.integers(1, 6),
+                 "medium": rng.integers(65, 800), "long": rng.integers(800, 3200)}[k])
+            for k in kind]
+    while sum(lens) > 5000:
+        lens = [x // 2 for x in lens]
+    gates = str(rng.choice(["strong", "mild", "none", "extreme"]))
+    inp = prefill_inputs(lens, hqk=hqk, hv=hv, seed=7200 + i,
+                         with_state=bool(rng.integers(0, 4) > 0),
+                         gates="strong" if gates == "extreme" else gates, state_std=0.05,
+                         cu_dtype=torch.int64 if rng.integers(0, 2) else torch.int32,
+                         pad_tokens=int(rng.choice([0, 0, 3, 70])))
+    if gates == "extreme":
+        inp = with_extreme_gates(inp, seed=7300 + i)
+    # segments per long sequence the launcher allows (1: whole-sequence scan)
+    G = 1
+    if n and n * hv * 3 <= 256:
+        G = 3
+        while G < 8 and n * hv * (2 * G - 1) <= 256:
+            G += 1
+    return inp, f"random {i}: hqk={hqk} hv={hv} gates={gates} segments<={G} lens={lens}"
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_prefill_random_cases(dev, i):
+    """Seeded random mixes that reach the planner's and the segment scan's branches
+    (1..8 segments, balanced and equal segment lengths, short and empty sequences next
+    to long ones) under every gate regime."""
+    inp, label = _random_case(i)
+    _run(dev, inp, label)
