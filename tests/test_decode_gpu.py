@@ -49,7 +49,7 @@ def test_decode_qk4_v8(dev, batch):
     _check(out, ns, ref_out, ref_ns, f"qk4_v8 B={batch}")
 
 
-@pytest.mark.parametrize("hqk,hv", [(8, 8), (2, 8), (1, 4)])
+@pytest.mark.parametrize("hqk,hv", [(8, 8), (2, 8), (1, 4), (2, 6), (1, 7), (3, 15)])
 def test_decode_head_ratios(dev, hqk, hv):
     inp = decode_inputs(5, hqk=hqk, hv=hv, seed=7)
     ref_out, ref_ns = _oracle(inp)
