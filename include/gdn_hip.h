@@ -60,7 +60,7 @@ typedef struct gdn_decode_params {
     int32_t batch;       /* B */
     int32_t seq_len;     /* T (1 in the reference's workloads) */
     int32_t num_qk_heads;
-    int32_t num_v_heads;
+    int32_t num_v_heads; /* a multiple of num_qk_heads, at most 65535 */
     int32_t head_size;   /* D */
     float scale;         /* readout scale; the caller resolves 0 -> 1/sqrt(D) */
     int32_t variant;     /* kernel variant for tuning sweeps; 0 = tuned default */

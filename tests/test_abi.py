@@ -86,7 +86,10 @@ def test_decode_rejects_bad_params_without_launch():
     assert "seq_len" in _lib.last_error()
     P.seq_len, P.num_v_heads = 1, 24  # 24 % 16 != 0
     assert lib.gdn_decode_launch(ctypes.byref(P), None) == _lib.GDN_EINVAL
-    P.num_v_heads = 32  # valid sizes but NULL tensors
+    P.num_qk_heads, P.num_v_heads = 1, 65536  # v-heads are a grid dimension (<= 65535)
+    assert lib.gdn_decode_launch(ctypes.byref(P), None) == _lib.GDN_EINVAL
+    assert "65535" in _lib.last_error()
+    P.num_qk_heads, P.num_v_heads = 16, 32  # valid sizes but NULL tensors
     assert lib.gdn_decode_launch(ctypes.byref(P), None) == _lib.GDN_EINVAL
     assert "NULL" in _lib.last_error()
     P.batch = 0  # empty batch is a no-op success
