@@ -1,8 +1,8 @@
 /*
  * CPU oracle for the Gated DeltaNet decode and prefill paths.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the smoke check
- * and the CPU-baseline leg of the benchmark load it. The product path (the HIP
+ * TEST INFRASTRUCTURE ONLY. Results are compared against this library: tests, the
+ * smoke check and the CPU-baseline leg of the benchmark load it. The product path (the HIP
  * library) never calls it, and nothing in the product falls back to it.
  *
  * It restates, token by token, the recurrence computed by the reference's

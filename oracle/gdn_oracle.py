@@ -1,7 +1,7 @@
 """CPU oracle for Gated DeltaNet decode / prefill.
 
 TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` and
-the ``cpu_baseline`` leg of ``bench.py`` as the checker. The product (the HIP
+the ``cpu_baseline`` leg of ``bench.py``, as the result to compare against. The product (the HIP
 library under ``mlsys26-flashinfer-ai-kernel-generation-contest_amd/``) never
 imports this module.
 

@@ -18,7 +18,7 @@ the reference's drivers and their external harness do for this path:
 * the scoring gate: any failing workload zeroes that kernel's score
   (computer_track_scores_local.py:157-158).
 
-    python tests/harness.py [--out gpurun_out/harness.json] [--quick]
+    python tests/harness.py [--out harness.json] [--quick]
 """
 from __future__ import annotations
 

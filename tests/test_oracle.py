@@ -1,4 +1,4 @@
-"""CPU tests pinning the oracle (oracle/gdn_oracle.*) before it is trusted as the checker.
+"""CPU tests pinning the oracle (oracle/gdn_oracle.*) before results are compared against it.
 
 The reference ships no golden vectors for this path, so the oracle is pinned by:
 * exact known answers (tests/golden/*.npz, computed in rational arithmetic by

@@ -23,7 +23,7 @@ def test_pack_metadata(name, entry):
     assert {"kernel.py", "gdn_hip/api.py", "csrc/gdn_prefill.hip", "csrc/gdn_prefill.h",
             "csrc/gdn_prefill_plan.hip", "csrc/gdn_prefill_prep.hip", "csrc/gdn_prefill_scan.hip",
             "include/gdn_hip.h"} <= paths
-    assert not any(p.startswith("oracle") for p in paths)  # the checker never ships
+    assert not any(p.startswith("oracle") for p in paths)  # the oracle never ships
     json.dumps(doc)
 
 
