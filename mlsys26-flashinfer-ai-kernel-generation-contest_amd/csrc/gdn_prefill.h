@@ -114,13 +114,32 @@ __device__ __forceinline__ float dpp_or0(float x)
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xF, true));
 }
 
+// dpp_or0 on 64-bit values (two 32-bit DPP moves)
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int64_t dpp_or0_b64(int64_t v)
+{
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true),
+              hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, ROWS, 0xF, true);
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
 template <int CTRL, int ROWS>
 __device__ __forceinline__ double dpp_or0_f64(double x)
 {
-    const int64_t v = __double_as_longlong(x);
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true),
-              hi = __builtin_amdgcn_update_dpp(0, (int)(v >> 32), CTRL, ROWS, 0xF, true);
-    return __longlong_as_double((int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+    return __longlong_as_double(dpp_or0_b64<CTRL, ROWS>(__double_as_longlong(x)));
+}
+
+// Inclusive prefix sum of int64 over the 64 lanes (the lane pattern of
+// wave_prefix_sum_pair below).
+__device__ __forceinline__ int64_t wave_prefix_sum_i64(int64_t x)
+{
+    x += dpp_or0_b64<0x111, 0xF>(x);
+    x += dpp_or0_b64<0x112, 0xF>(x);
+    x += dpp_or0_b64<0x114, 0xF>(x);
+    x += dpp_or0_b64<0x118, 0xF>(x);
+    x += dpp_or0_b64<0x142, 0xA>(x);
+    x += dpp_or0_b64<0x143, 0xC>(x);
+    return x;
 }
 
 // Inclusive prefix sum over the 64 lanes: shifts by 1, 2, 4, 8 inside each 16-lane row,

@@ -11,7 +11,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
         // Chunk counts are clamped so that malformed (non-monotone) cu_seqlens can
         // never index past the chunk tables or records sized for nc chunks; for
         // valid input sum(ceil(len / C)) <= ceil(T / C) + N = nc always holds.
-        __shared__ int64_t scan[256];
+        __shared__ int64_t s_wtot[4];  // per-wave totals of the block scan
         __shared__ int32_t s_nck[kPlanSortMax];
         // up to kPlanSortMax sequences the chunk table is filled chunk-parallel from these
         __shared__ int32_t s_first[kPlanSortMax], s_end[kPlanSortMax], s_t0[kPlanSortMax],
@@ -36,15 +36,15 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                 if (n < kPlanSortMax)
                     s_nck[n] = nck;
             }
-            scan[tid] = nck;
+            // inclusive prefix sum over the block: DPP inside each wave, then the totals
+            // of the waves before this one
+            int64_t incl = wave_prefix_sum_i64(nck);
+            if ((tid & 63) == 63)
+                s_wtot[tid >> 6] = incl;
             __syncthreads();
-            for (int off = 1; off < 256; off <<= 1) {
-                const int64_t add = tid >= off ? scan[tid - off] : 0;
-                __syncthreads();
-                scan[tid] += add;
-                __syncthreads();
-            }
-            const int64_t first = s_carry + scan[tid] - nck;
+            for (int w2 = 0; w2 < (tid >> 6); ++w2)
+                incl += s_wtot[w2];
+            const int64_t first = s_carry + incl - nck;
             if (n < p.N) {
                 p.seq_chunk0[n] = (int32_t)(first < p.nc ? first : p.nc);
                 if (par) {
@@ -59,9 +59,9 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                     }
                 }
             }
-            __syncthreads();
+            __syncthreads();  // every lane has read s_carry and s_wtot
             if (tid == 255)
-                s_carry += scan[255];
+                s_carry += incl;
             __syncthreads();
         }
         if (tid == 0) {
