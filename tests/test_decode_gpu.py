@@ -227,3 +227,27 @@ def test_decode_extreme_gates(dev, seq_len):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all() and torch.isfinite(ns).all()
     _check(out, ns, ref_out, ref_ns, f"extreme gates T={seq_len}")
+
+
+def test_decode_state_offsets_beyond_32_bits(dev):
+    """A state view whose batch stride is 2^31 elements takes the kernel's 64-bit offset
+    instantiation (every other test fits 32-bit offsets)."""
+    inp = decode_inputs(2, seed=77)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    n = 32 * 128 * 128
+    big = torch.empty((1 << 31) + n, dtype=torch.float32, device=dev)  # 8 GiB
+    try:
+        st = big.as_strided((2, 32, 128, 128), (1 << 31, 128 * 128, 128, 1))
+        st.copy_(g.state)
+        out, ns = gdn_decode(g.q, g.k, g.v, st, g.A_log, g.a, g.dt_bias, g.b, g.scale)
+        torch.cuda.synchronize()
+        _check(out, ns, ref_out, ref_ns, "state batch stride 2^31")
+        inpl_out, inpl_ns = gdn_decode(g.q, g.k, g.v, st, g.A_log, g.a, g.dt_bias, g.b, g.scale,
+                                       new_state=st)
+        torch.cuda.synchronize()
+        assert inpl_ns.data_ptr() == st.data_ptr()
+        _check(inpl_out, st.clone(), ref_out, ref_ns, "state batch stride 2^31, in place")
+    finally:
+        del big
+        torch.cuda.empty_cache()
