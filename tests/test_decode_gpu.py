@@ -251,3 +251,21 @@ def test_decode_state_offsets_beyond_32_bits(dev):
     finally:
         del big
         torch.cuda.empty_cache()
+
+
+def test_decode_more_sequences_than_one_grid(dev):
+    """B above 65535 is launched in slices of at most 65535 sequences (a grid dimension);
+    sequences on both sides of the slice boundary match the oracle."""
+    B = 65537
+    inp = decode_inputs(B, hqk=1, hv=1, seed=91)  # one head: 4 GiB of fp32 state
+    g = inp.to(dev)
+    out, ns = gdn_decode(*g.args())
+    torch.cuda.synchronize()
+    idx = torch.tensor([0, 1, 65533, 65534, 65535, 65536])
+    sub = type(inp)(inp.q[idx], inp.k[idx], inp.v[idx], inp.state[idx], inp.A_log, inp.a[idx],
+                    inp.dt_bias, inp.b[idx], inp.scale)
+    ref_out, ref_ns = _oracle(sub)
+    di = idx.to(dev)
+    _check(out[di], ns[di], ref_out, ref_ns, f"B={B}, sequences {idx.tolist()}")
+    del g, out, ns
+    torch.cuda.empty_cache()
