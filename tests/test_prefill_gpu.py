@@ -306,3 +306,11 @@ def test_prefill_random_cases(dev, i):
     to long ones) under every gate regime."""
     inp, label = _random_case(i)
     _run(dev, inp, label)
+
+
+def test_prefill_long_sequence_64k(dev):
+    """One 65536-token sequence (1024 chunks): eight segments of ~128 chunks with their state
+    chain, mild decay so every segment's state carries into the next."""
+    inp = prefill_inputs([65536], hqk=1, hv=2, seed=97, with_state=True, gates="mild",
+                         state_std=0.05)
+    _run(dev, inp, "1 x 65536, hqk=1 hv=2")
