@@ -269,3 +269,35 @@ def test_decode_more_sequences_than_one_grid(dev):
     _check(out[di], ns[di], ref_out, ref_ns, f"B={B}, sequences {idx.tolist()}")
     del g, out, ns
     torch.cuda.empty_cache()
+
+
+def test_decode_plan_in_graph(dev):
+    """A DecodePlan step captured in a HIP graph: every replay, with eager work and a sync
+    between replays, reproduces the eager launch bit for bit."""
+    from gdn_hip.api import DecodePlan
+    inp = decode_inputs(16, seed=301)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out, ns = torch.empty_like(g.v), torch.empty_like(g.state)
+    plan = DecodePlan(g.q, g.k, g.v, g.state, g.A_log, g.a, g.dt_bias, g.b, g.scale, out, ns)
+    plan.run()
+    torch.cuda.synchronize()
+    _check(out, ns, ref_out, ref_ns, "eager")
+    eager_out, eager_ns = out.clone(), ns.clone()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        plan.run()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run()
+    for r in range(3):
+        out.zero_()
+        ns.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_out), f"replay {r}: output differs"
+        assert torch.equal(ns, eager_ns), f"replay {r}: new_state differs"
