@@ -338,3 +338,35 @@ def test_prefill_and_decode_on_concurrent_streams(dev):
     _check(oa, na, *ref_a, "stream 1 prefill")
     _check(ob, nb, *ref_b, "stream 2 prefill")
     _check(od, nd, *ref_d, "stream 3 decode")
+
+
+def test_prefill_in_graph(dev):
+    """gdn_prefill captured in a HIP graph (plan, prep and scan launches): every replay, with
+    eager work and a sync between replays, reproduces the eager call bit for bit."""
+    inp = prefill_inputs([500, 64, 1300, 7], seed=311, with_state=True)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    T, N = g.q.shape[0], len(inp.seqlens)
+    out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((N, 32, 128, 128), dtype=torch.float32, device=dev)
+    gdn_prefill(*g.args(), output=out, new_state=ns)
+    torch.cuda.synchronize()
+    _check(out, ns, ref_out, ref_ns, "eager")
+    eager_out, eager_ns = out.clone(), ns.clone()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        gdn_prefill(*g.args(), output=out, new_state=ns)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gdn_prefill(*g.args(), output=out, new_state=ns)
+    for r in range(3):
+        out.zero_()
+        ns.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_out), f"replay {r}: output differs"
+        assert torch.equal(ns, eager_ns), f"replay {r}: new_state differs"
