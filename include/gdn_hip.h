@@ -3,7 +3,10 @@
  *
  * Plain C: raw device pointers, element strides and sizes; no torch types.
  * Every entry point returns 0 on success or a negative GDN_E* code, in which
- * case gdn_last_error() describes the failure (per calling thread). Launches are
+ * case gdn_last_error() describes the failure (per calling thread; each call clears
+ * it first, and drains any HIP error an earlier call left pending). Argument errors
+ * are reported before anything is launched; after GDN_ELAUNCH, kernels launched
+ * before the failing one may already have written part of the outputs. Launches are
  * asynchronous on the given stream (a hipStream_t; NULL = the default stream);
  * nothing here allocates, frees or synchronises caller memory.
  *
@@ -38,7 +41,7 @@ extern "C" {
 /* Version of this ABI (GDN_HIP_ABI_VERSION of the build). */
 int gdn_abi_version(void);
 
-/* Message for the last failing call made by this thread ("" if none). */
+/* Message of this thread's last call ("" if it succeeded). */
 const char *gdn_last_error(void);
 
 /*

@@ -17,6 +17,15 @@ int gdn_set_error(int code, const char *fmt, ...)
     return code;
 }
 
+void gdn_begin_call() { g_last_error[0] = '\0'; }
+
+void gdn_begin_launches()
+{
+    // Drain an error an earlier HIP call left on this thread (a previous framework op),
+    // so that the checks after this call's launches report only its own.
+    (void)hipGetLastError();
+}
+
 int gdn_check_launch(const char *what)
 {
     hipError_t e = hipGetLastError();

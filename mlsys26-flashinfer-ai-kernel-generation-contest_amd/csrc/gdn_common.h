@@ -77,3 +77,7 @@ __device__ __forceinline__ float group16_sum(float x)
 // Host-side error channel (gdn_abi.hip).
 int gdn_set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int gdn_check_launch(const char *what);
+// Start of every C-ABI entry point: clears the last-error message.
+void gdn_begin_call();
+// After argument checks, before the first launch: drains a stale HIP error.
+void gdn_begin_launches();

@@ -235,6 +235,7 @@ int launch_grid(DecodeArgs<I> a, int B, int HV, hipStream_t stream)
     const int64_t gx = (int64_t)a.T * kNVT;
     if (gx > 0x7fffffff)
         return gdn_set_error(GDN_EINVAL, "gdn_decode: seq_len %d too large", a.T);
+    gdn_begin_launches();
     for (int b0 = 0; b0 < B; b0 += 65535) {
         a.b0 = b0;
         const dim3 grid((unsigned)gx, (unsigned)HV, (unsigned)std::min(65535, B - b0));
@@ -302,6 +303,7 @@ bool aligned(const void *p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
 extern "C" int gdn_decode_launch(const gdn_decode_params *p, void *stream)
 {
+    gdn_begin_call();
     if (!p || p->struct_size != (int32_t)sizeof(gdn_decode_params))
         return gdn_set_error(GDN_EINVAL, "gdn_decode: params NULL or struct_size mismatch");
     const int B = p->batch, T = p->seq_len, HQK = p->num_qk_heads, HV = p->num_v_heads,

@@ -102,6 +102,7 @@ extern "C" int64_t gdn_prefill_workspace_size(int32_t total_tokens, int32_t num_
                                               int32_t num_qk_heads, int32_t num_v_heads,
                                               int32_t head_size)
 {
+    gdn_begin_call();
     if (total_tokens < 0 || num_seqs < 0 || num_qk_heads <= 0 || num_v_heads <= 0 ||
         num_v_heads % num_qk_heads != 0 || head_size != 128)
         return gdn_set_error(GDN_EINVAL, "gdn_prefill_workspace_size: bad sizes T=%d N=%d "
@@ -112,6 +113,7 @@ extern "C" int64_t gdn_prefill_workspace_size(int32_t total_tokens, int32_t num_
 
 extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
 {
+    gdn_begin_call();
     if (!p || p->struct_size != (int32_t)sizeof(gdn_prefill_params))
         return gdn_set_error(GDN_EINVAL, "gdn_prefill: params NULL or struct_size mismatch");
     const int T = p->total_tokens, N = p->num_seqs, HQK = p->num_qk_heads,
@@ -201,6 +203,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     pa.seg_G = G;
     pa.seg_capA = (int)L.capA;
     pa.jobs = G > 1 ? (int32_t *)(ws + L.jobs) : nullptr;
+    gdn_begin_launches();
     hipLaunchKernelGGL(gdn::gdn_prefill_plan_kernel, dim3(1 + kZeroFillBlocks), dim3(256), 0,
                        st, pa);
     int rc = gdn_check_launch("gdn_prefill_plan_kernel");

@@ -51,6 +51,11 @@ def _resolve_scale(scale, D):
     if scale is None:
         return 1.0 / math.sqrt(D)
     if isinstance(scale, torch.Tensor):
+        # the reference types scale as a float (gdn_decode/solution/triton/kernel.py:230);
+        # a device tensor is read back, a host sync a captured graph cannot record
+        if scale.is_cuda and torch.cuda.is_current_stream_capturing():
+            raise ValueError("scale must be a Python float while a HIP graph is being "
+                             "captured (a tensor scale is read back with a device sync)")
         scale = float(scale.item())
     scale = float(scale)
     return 1.0 / math.sqrt(D) if scale == 0.0 else scale
@@ -252,11 +257,23 @@ def set_prefill_variant(v: int) -> None:
 
 _ws_lock = threading.Lock()
 _ws_cache: dict = {}
+_graph_ws: list = []
 
 
-def _workspace(dev, stream_id, nbytes):
-    """Grow-only device workspace per (device, stream); rewritten by every call."""
-    key = (dev.index, stream_id)
+def _workspace(dev, stream, nbytes):
+    """Device workspace for one prefill call.
+
+    Eager calls share a grow-only buffer per (device, stream), rewritten by every call
+    (stream order keeps calls on one stream apart). A call being captured into a HIP
+    graph gets a buffer of its own that is never freed or reused: the graph's kernels
+    keep pointing at it for as long as the graph may be replayed, and graphs captured
+    on the shared capture stream must not share (or free) one another's workspace."""
+    if torch.cuda.is_current_stream_capturing():
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        with _ws_lock:
+            _graph_ws.append(buf)
+        return buf
+    key = (dev.index, stream.cuda_stream)
     with _ws_lock:
         buf = _ws_cache.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -265,19 +282,22 @@ def _workspace(dev, stream_id, nbytes):
         return buf
 
 
-@torch.no_grad()
-def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=None,
-                new_state=None):
-    """Gated DeltaNet prefill over packed variable-length sequences.
+def release_workspace() -> None:
+    """Drop the cached eager prefill workspaces (they return to torch's caching
+    allocator once in-flight calls on their streams are done with them: the caller
+    synchronises first). Workspaces of captured graphs are kept."""
+    with _ws_lock:
+        _ws_cache.clear()
 
-    q, k: bf16 [T, HQK, D]; v: bf16 [T, HV, D]; state: fp32 [N, HV, D, D] or None;
-    A_log, dt_bias: fp32 [HV]; a, b: bf16 [T, HV]; cu_seqlens: int32/int64 [N+1];
-    scale: float (None/0 -> 1/sqrt(D)). Returns (output bf16 [T, max(HQK,HV), D],
-    new_state fp32 [N, HV, D, D]).
-    Mirrors gdn_prefill/solution/triton/kernel.py:253-337 (argument order :254,
-    defaults and DPS handling :276-302), generalised from the 4/8 head layout it
-    asserts (:271-274) to any HV that is a multiple of HQK.
-    """
+
+def _prefill_marshal(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                     new_state, with_workspace=True):
+    """Validate like the reference host wrapper and build the ABI params.
+
+    Returns ((output, new_state),) when there is nothing to launch (empty input, handled
+    here as gdn_prefill/solution/triton/kernel.py:286-302 does), else (params, output,
+    new_state, copy_back, keep, stream) as _decode_marshal does. ``with_workspace=False``
+    leaves the workspace fields empty (for gdn_prefill_launch_noalloc)."""
     _need_tensor("q", q, torch.bfloat16, 3)
     T, HQK, D = q.shape
     _need_tensor("k", k, torch.bfloat16, 3)
@@ -329,7 +349,7 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=
             new_state.zero_()
         elif new_state.data_ptr() != state.data_ptr():
             new_state.copy_(state)
-        return output, new_state
+        return ((output, new_state),)
 
     qk_ok = (16, 8)
     st_ok = (16, 4)
@@ -345,11 +365,13 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=
         st_ = st_.clone()
 
     lib = _lib.load()
-    ws_bytes = int(lib.gdn_prefill_workspace_size(T, N, HQK, HV, D))
-    if ws_bytes < 0:
-        raise RuntimeError(f"gdn_prefill_workspace_size failed: {_lib.last_error()}")
     stream = torch.cuda.current_stream(dev)
-    ws = _workspace(dev, stream.cuda_stream, ws_bytes)
+    ws = None
+    if with_workspace:
+        ws_bytes = int(lib.gdn_prefill_workspace_size(T, N, HQK, HV, D))
+        if ws_bytes < 0:
+            raise RuntimeError(f"gdn_prefill_workspace_size failed: {_lib.last_error()}")
+        ws = _workspace(dev, stream, ws_bytes)
 
     P = _lib.PrefillParams()
     P.struct_size = ctypes.sizeof(_lib.PrefillParams)
@@ -368,12 +390,34 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=
     P.cu_seqlens = _ptr(cu_)
     P.output, P.output_stride = _ptr(out_), _strides(out_, 3)
     P.new_state, P.new_state_stride = _ptr(ns_), _strides(ns_, 4)
-    P.workspace, P.workspace_bytes = _ptr(ws), ws.numel()
-    with torch.cuda.device(dev):
-        _lib.check(lib.gdn_prefill_launch(ctypes.byref(P), ctypes.c_void_p(stream.cuda_stream)),
+    P.workspace, P.workspace_bytes = (_ptr(ws), ws.numel()) if ws is not None else (None, 0)
+    copy_back = [(u, t) for u, t in ((output, out_), (new_state, ns_)) if t is not u]
+    keep = (q_, k_, v_, st_, A_log, a_, dt_bias, b_, cu_, out_, ns_, ws)
+    return P, output, new_state, copy_back, keep, stream
+
+
+@torch.no_grad()
+def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=None,
+                new_state=None):
+    """Gated DeltaNet prefill over packed variable-length sequences.
+
+    q, k: bf16 [T, HQK, D]; v: bf16 [T, HV, D]; state: fp32 [N, HV, D, D] or None;
+    A_log, dt_bias: fp32 [HV]; a, b: bf16 [T, HV]; cu_seqlens: int32/int64 [N+1];
+    scale: float (None/0 -> 1/sqrt(D)). Returns (output bf16 [T, max(HQK,HV), D],
+    new_state fp32 [N, HV, D, D]).
+    Mirrors gdn_prefill/solution/triton/kernel.py:253-337 (argument order :254,
+    defaults and DPS handling :276-302), generalised from the 4/8 head layout it
+    asserts (:271-274) to any HV that is a multiple of HQK.
+    """
+    m = _prefill_marshal(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                         new_state)
+    if len(m) == 1:  # nothing to launch
+        return m[0]
+    P, output, new_state, copy_back, _keep, stream = m
+    with torch.cuda.device(q.device):
+        _lib.check(_lib.load().gdn_prefill_launch(ctypes.byref(P),
+                                                  ctypes.c_void_p(stream.cuda_stream)),
                    "gdn_prefill_launch")
-    if out_ is not output:
-        output.copy_(out_)
-    if ns_ is not new_state:
-        new_state.copy_(ns_)
+    for user, tmp in copy_back:
+        user.copy_(tmp)
     return output, new_state

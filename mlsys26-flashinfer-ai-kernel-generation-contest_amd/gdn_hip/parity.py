@@ -5,9 +5,12 @@ The contest rule (FAQ.md:104-110): an element fails only if BOTH
 matched fraction reaches ``required_matched_ratio`` (1.0 for GDN). A failing
 workload zeroes the kernel's score (computer_track_scores_local.py:157-158).
 
-Tolerances used for this path:
-* output (bf16):    atol = rtol = 2e-2
-* new_state (fp32): rtol = 1e-3, atol = 1e-4 (states are O(0.01..3))
+Bars used for this path (every test, the harness and smoke()):
+* output (bf16):    atol = rtol = 1e-2, the contest's GDN tolerance (FAQ.md:104-110);
+                    tighter than the 2e-2 the benchmark specification allows.
+* new_state (fp32): elementwise atol = 1e-4, rtol = 1e-3 (both-condition rule), AND the
+                    normwise relative error ||x - ref|| / ||ref|| <= 1e-3 ("1e-3 relative
+                    on fp32 new_state"). The contest itself holds new_state to 1e-2.
 """
 from __future__ import annotations
 
@@ -15,8 +18,11 @@ from dataclasses import dataclass
 
 import numpy as np
 
-OUT_TOL = dict(atol=2e-2, rtol=2e-2)
+# gdn (DSA / GDN) row of FAQ.md:104-110
+CONTEST_TOL = dict(atol=1e-2, rtol=1e-2)
+OUT_TOL = dict(CONTEST_TOL)
 STATE_TOL = dict(atol=1e-4, rtol=1e-3)
+STATE_NORM_RTOL = 1e-3
 
 
 @dataclass
@@ -27,10 +33,12 @@ class Verdict:
     n_fail: int
     n: int
     norm_rel: float
+    norm_bar: float | None = None  # normwise bar applied (None: elementwise only)
 
     def __str__(self):
+        bar = "" if self.norm_bar is None else f" (<= {self.norm_bar:g})"
         return (f"{'PASSED' if self.ok else 'FAILED'} max_abs={self.max_abs:.3e} "
-                f"max_rel={self.max_rel:.3e} norm_rel={self.norm_rel:.3e} "
+                f"max_rel={self.max_rel:.3e} norm_rel={self.norm_rel:.3e}{bar} "
                 f"fail={self.n_fail}/{self.n}")
 
 
@@ -43,7 +51,10 @@ def _np(x):
     return np.asarray(x, dtype=np.float64)
 
 
-def compare(actual, expected, atol, rtol, required_matched_ratio=1.0) -> Verdict:
+def compare(actual, expected, atol, rtol, required_matched_ratio=1.0,
+            norm_rtol=None) -> Verdict:
+    """Both-condition elementwise rule; with ``norm_rtol`` the normwise relative error
+    must also stay within it (an all-zero reference then needs an all-zero result)."""
     a, e = _np(actual), _np(expected)
     if a.shape != e.shape:
         raise ValueError(f"shape mismatch {a.shape} vs {e.shape}")
@@ -56,11 +67,13 @@ def compare(actual, expected, atol, rtol, required_matched_ratio=1.0) -> Verdict
     nf = int(fail.sum())
     ok = n == 0 or (1.0 - nf / n) >= required_matched_ratio
     en = float(np.linalg.norm(e))
+    dn = float(np.linalg.norm(np.where(finite, a - e, np.inf)))
+    norm_rel = dn / en if en > 0 else dn
+    if norm_rtol is not None and n:
+        ok = ok and (norm_rel <= norm_rtol if en > 0 else dn == 0.0)
     return Verdict(ok=ok, max_abs=float(d.max()) if n else 0.0,
                    max_rel=float(rel[np.isfinite(rel)].max()) if n and np.isfinite(rel).any()
-                   else 0.0, n_fail=nf, n=n,
-                   norm_rel=float(np.linalg.norm(a - e) / en) if en > 0 else float(
-                       np.linalg.norm(a - e)))
+                   else 0.0, n_fail=nf, n=n, norm_rel=norm_rel, norm_bar=norm_rtol)
 
 
 def check_output(actual, expected) -> Verdict:
@@ -68,4 +81,4 @@ def check_output(actual, expected) -> Verdict:
 
 
 def check_state(actual, expected) -> Verdict:
-    return compare(actual, expected, **STATE_TOL)
+    return compare(actual, expected, **STATE_TOL, norm_rtol=STATE_NORM_RTOL)

@@ -6,8 +6,9 @@ the reference's drivers and their external harness do for this path:
 * workloads per definition, each called destination-passing style with
   preallocated ``output`` / ``new_state`` (README.md:227-257);
 * correctness: an element fails only if both ``|err| > atol`` and ``|err| > rtol |ref|``,
-  a workload passes at matched ratio 1.0 (FAQ.md:104-110); tolerances here are the
-  ones this path is held to (output 2e-2, state rtol 1e-3 / atol 1e-4);
+  a workload passes at matched ratio 1.0 (FAQ.md:104-110); output at the contest's
+  atol = rtol = 1e-2, new_state at the tighter bar this path is held to (elementwise
+  rtol 1e-3 / atol 1e-4 and normwise 1e-3, gdn_hip.parity);
 * timing: warmup / iterations / trials = 3 / 100 / 5 for decode and 1 / 10 / 3 for
   prefill (gdn_decode/scripts/run_local.py:33, gdn_prefill/scripts/run_local.py:33),
   median trial, HIP events on the launch stream;
@@ -40,7 +41,7 @@ import torch  # noqa: E402
 
 from gdn_hip import gdn_decode, gdn_prefill  # noqa: E402
 from gdn_hip.inputs import decode_inputs, prefill_inputs, varlen_lengths  # noqa: E402
-from gdn_hip.parity import OUT_TOL, STATE_TOL, compare  # noqa: E402
+from gdn_hip.parity import check_output, check_state  # noqa: E402
 from oracle import gdn_oracle as O  # noqa: E402
 
 SOLUTION = "mi355x-hip"
@@ -115,8 +116,8 @@ def run_workload(kind, inp, dev):
         torch.cuda.synchronize()
     except Exception as exc:  # the harness reports, it does not raise
         return dict(status="RUNTIME_ERROR", solution=SOLUTION, error=str(exc))
-    vo = compare(out, ref_out, **OUT_TOL)
-    vs = compare(ns, ref_ns, **STATE_TOL)
+    vo = check_output(out, ref_out)
+    vs = check_state(ns, ref_ns)
     status = "PASSED" if (vo.ok and vs.ok) else "INCORRECT_NUMERICAL"
     lat = _time_gpu(call, cfg)
     return dict(status=status, solution=SOLUTION, latency_ms=lat, reference_latency_ms=ref_ms,

@@ -33,8 +33,9 @@ def test_packed_solution_builds_and_imports(tmp_path):
         dst = tmp_path / src["path"]
         dst.parent.mkdir(parents=True, exist_ok=True)
         dst.write_text(src["content"])
-    code = ("import sys, ctypes; sys.path.insert(0, %r); import kernel; "
-            "from gdn_hip import build; lib = ctypes.CDLL(build.LIB_PATH); "
+    # the solution's build step, then the harness's import (which does not compile)
+    code = ("import sys, ctypes; sys.path.insert(0, %r); from gdn_hip import build; "
+            "build.build(); import kernel; lib = ctypes.CDLL(build.LIB_PATH); "
             "print(all(hasattr(lib, s) for s in %r), kernel.gdn_prefill.__name__)"
             % (str(tmp_path), list(EXPORTED)))
     res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
@@ -42,3 +43,25 @@ def test_packed_solution_builds_and_imports(tmp_path):
     assert res.returncode == 0, res.stderr[-2000:]
     assert res.stdout.split() == ["True", "gdn_prefill"]
     assert os.path.exists(tmp_path / "gdn_hip" / "libgdn_hip.so")
+
+
+def test_packed_entry_refuses_to_compile_on_import(tmp_path):
+    """Without the build step the entry module raises instead of compiling inside the
+    harness's (possibly timed) process."""
+    doc = pack.pack_solution("gdn_decode")
+    for src in doc["sources"]:
+        dst = tmp_path / src["path"]
+        dst.parent.mkdir(parents=True, exist_ok=True)
+        dst.write_text(src["content"])
+    code = "import sys; sys.path.insert(0, %r); import kernel" % str(tmp_path)
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         timeout=300, cwd=str(tmp_path))
+    assert res.returncode != 0 and "not built" in res.stderr
+    assert not os.path.exists(tmp_path / "gdn_hip" / "libgdn_hip.so")
+
+
+def test_solution_language_is_one_the_reference_lists():
+    """FAQ.md:53-56 maps language = "python" to solution/python/ (next to triton and
+    cuda), and FAQ.md:138 points kernels with their own build at a Python solution."""
+    for name in ("gdn_decode", "gdn_prefill"):
+        assert pack.pack_solution(name)["spec"]["language"] in ("python", "triton", "cuda")
