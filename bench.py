@@ -5,12 +5,16 @@ Prints ONE JSON line. Headline (``value``): decode at 64 sequences x 1 token
 timed with HIP events on the launch stream over K back-to-back steps. A step is
 one decode over the whole batch; four distinct buffer sets rotate so that the
 256 MiB working set of one step cannot stay resident in the 256 MB Infinity
-Cache between steps. The ``prefill`` object reports the 16-sequence varlen
-workload (lengths ~ U[64, 1024] from seed 0, non-zero initial state) as Mtok/s
-and algorithmic bf16 MFMA TFLOP/s. ``cpu_baseline`` times the CPU oracle on the
-host cores over a bounded sample.
+Cache between steps. Beside it: ``decode_b1`` (1 sequence, the latency case),
+``decode_b256_inplace`` (256 sequences, state updated in place), ``prefill`` (16
+sequences, lengths ~ U[64, 1024] from seed 0, non-zero initial state) and
+``prefill_single_4k`` (one 4096-token sequence, zero state), the prefills as Mtok/s and
+algorithmic bf16 MFMA TFLOP/s. ``cpu_baseline`` times the fp32 CPU oracle on the host
+cores over a bounded sample of the headline workload; ``cpu_baseline_more`` does the
+same for the 1-sequence decode and the 16-sequence prefill.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py --trace-summary <rocprofv3 kernel_trace.csv> [--skip-first N]
 """
 from __future__ import annotations
 
@@ -50,7 +54,9 @@ def _traffic_from_profile(name):
     return None
 
 
-def bench_decode(steps, warmup, batch=64, nsets=4):
+def bench_decode(steps, warmup, batch=64, nsets=4, inplace=False):
+    """Decode over `nsets` rotating buffer sets (pre-marshalled DecodePlans, HIP events
+    on the launch stream); `inplace`: new_state is the state buffer itself."""
     import torch
 
     from gdn_hip.api import DecodePlan
@@ -64,7 +70,8 @@ def bench_decode(steps, warmup, batch=64, nsets=4):
         plans.append(DecodePlan(base.q.clone(), base.k.clone(), base.v.clone(), st,
                                 base.A_log, base.a.clone(), base.dt_bias, base.b.clone(),
                                 base.scale, torch.empty_like(base.v),
-                                torch.empty_like(st)))
+                                st if inplace else torch.empty_like(st)))
+    del base
     stream = torch.cuda.current_stream(dev)
     for i in range(warmup):
         plans[i % nsets].run()
@@ -83,6 +90,8 @@ def bench_decode(steps, warmup, batch=64, nsets=4):
     ms = statistics.median(trials)
     nbytes = decode_bytes(batch)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    del plans
+    torch.cuda.empty_cache()
     return dict(ms=ms, gbs=gbs, bytes=nbytes, trials=trials)
 
 
@@ -121,31 +130,80 @@ def bench_prefill(steps, warmup, lens=None, with_state=True):
                 mfma_frac=tflops / BF16_PEAK_TFLOPS)
 
 
+def _host_cores():
+    """(threads used, cores this process may run on, cores of the host)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(avail, 16)), avail, os.cpu_count() or avail
+
+
+def _time_cpu(fn, budget_s, max_n=200):
+    fn()  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= max_n:
+            return el / n, n
+
+
 def cpu_baseline_decode(batch=64, budget_s=10.0):
     """Time the float32 C oracle (a port of the reference arithmetic) on the host cores
     over repeated full decode steps, up to ~budget_s seconds."""
     from gdn_hip.inputs import decode_bytes, decode_inputs
     from oracle import gdn_oracle as O
 
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
+    cores, avail, total = _host_cores()
     inp = decode_inputs(batch, seed=0)
     args = (inp.q, inp.k, inp.v, inp.state, inp.A_log, inp.a, inp.dt_bias, inp.b, inp.scale)
-    O.decode(*args, precision="f32", threads=cores)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.decode(*args, precision="f32", threads=cores)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 200:
-            break
-    sec = el / n
-    return dict(value=decode_bytes(batch) / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+    sec, n = _time_cpu(lambda: O.decode(*args, precision="f32", threads=cores), budget_s)
+    return dict(value=decode_bytes(batch) / sec / 1e9, unit="GB/s", cores=cores,
+                cores_available=avail, cores_host=total, kind="port",
+                us_per_step=sec * 1e6,
                 sample=f"{n} full decode steps (B={batch}, fp32 C oracle, OpenMP over "
-                       f"(sequence, v-head)); {sec * 1e3:.1f} ms/step")
+                       f"(sequence, v-head)); {sec * 1e3:.2f} ms/step")
+
+
+def cpu_baseline_prefill(budget_s=5.0):
+    """The fp32 C oracle on the whole 16-sequence prefill (token recurrence, OpenMP over
+    (sequence, v-head)), repeated up to ~budget_s seconds."""
+    from gdn_hip.inputs import prefill_inputs, varlen_lengths
+    from oracle import gdn_oracle as O
+
+    cores, avail, total = _host_cores()
+    lens = varlen_lengths(16, seed=0)
+    inp = prefill_inputs(lens, seed=0, with_state=True)
+    sec, n = _time_cpu(lambda: O.prefill(*inp.args(), precision="f32", threads=cores),
+                       budget_s, max_n=50)
+    T = sum(lens)
+    return dict(value=T / sec / 1e6, unit="Mtok/s", cores=cores, cores_available=avail,
+                cores_host=total, kind="port", us_per_step=sec * 1e6,
+                sample=f"{n} full prefills (16 sequences, T={T}, fp32 C oracle); "
+                       f"{sec * 1e3:.1f} ms/step")
+
+
+def summarize_trace(path, skip_first=0):
+    """Per-kernel dispatch durations from a rocprofv3 kernel_trace.csv, dropping each
+    kernel's first `skip_first` dispatches (the warmup calls); prints a markdown table."""
+    import csv
+    from collections import defaultdict
+
+    per = defaultdict(list)
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            per[row["Kernel_Name"]].append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    print(f"| kernel | dispatches (after skipping {skip_first}) | avg us | min us | max us |")
+    print("|---|---|---|---|---|")
+    for name, d in sorted(per.items(), key=lambda kv: -sum(kv[1][skip_first:])):
+        d = d[skip_first:]
+        if not d:
+            continue
+        short = name.split("(")[0][:90]
+        print(f"| `{short}` | {len(d)} | {sum(d) / len(d) / 1e3:.2f} | {min(d) / 1e3:.2f} | "
+              f"{max(d) / 1e3:.2f} |")
 
 
 def main():
@@ -155,12 +213,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all",
+    ap.add_argument("--cpu-budget", type=float, default=6.0)
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "prefill4k"], default="all",
                     help="run one path only (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also launch a plain 256 MiB device copy (rocprof counter calibration)")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="summarise a rocprofv3 kernel_trace.csv per kernel and exit")
+    ap.add_argument("--skip-first", type=int, default=0,
+                    help="with --trace-summary: dispatches to drop per kernel (warmup)")
     args = ap.parse_args()
+    if args.trace_summary:
+        summarize_trace(args.trace_summary, args.skip_first)
+        return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this path runs on one GPU "
               "(every (sequence, head) state is independent; see the sharding notes).",
@@ -172,6 +237,7 @@ def main():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
     from gdn_hip import _lib
+    from gdn_hip.inputs import prefill_bytes
 
     _lib.load()
     if args.calibrate_copy:
@@ -182,8 +248,11 @@ def main():
         torch.cuda.synchronize()
         log("copy calibration: 3 x 268435456-byte device copies")
         del src, dst
-    if args.only == "prefill":
-        pre = bench_prefill(max(3, min(args.steps, 50)), 2)
+    psteps = max(3, min(args.steps, 50))
+    pwarm = 5
+    if args.only in ("prefill", "prefill4k"):
+        lens, st = (None, True) if args.only == "prefill" else ([4096], False)
+        pre = bench_prefill(psteps, pwarm, lens=lens, with_state=st)
         log(f"prefill: T={pre['tokens']} {pre['ms'] * 1e3:.1f} us/step "
             f"{pre['mtok_s']:.1f} Mtok/s {pre['tflops']:.1f} TFLOP/s")
         return
@@ -192,20 +261,29 @@ def main():
     log(f"decode: {dec['ms'] * 1e3:.2f} us/step, {dec['gbs']:.0f} GB/s (trials {dec['trials']})")
     if args.only == "decode":
         return
-    pre = None
+    dec1 = bench_decode(args.steps, args.warmup, batch=1, nsets=16)
+    log(f"decode B=1: {dec1['ms'] * 1e3:.2f} us/step")
+    dec256 = bench_decode(max(10, args.steps // 4), max(2, args.warmup // 4), batch=256, nsets=2,
+                          inplace=True)
+    log(f"decode B=256 in place: {dec256['ms'] * 1e3:.2f} us/step, {dec256['gbs']:.0f} GB/s")
+    pre = pre4k = None
     if not args.no_prefill:
-        psteps = max(3, min(args.steps, 50))
-        log(f"prefill 16x varlen: warmup 2, steps {psteps}")
-        pre = bench_prefill(psteps, 2)
+        log(f"prefill 16x varlen: warmup {pwarm}, steps {psteps}")
+        pre = bench_prefill(psteps, pwarm)
         log(f"prefill: T={pre['tokens']} {pre['ms'] * 1e3:.1f} us/step "
             f"{pre['mtok_s']:.1f} Mtok/s {pre['tflops']:.1f} TFLOP/s")
-        pre4k = bench_prefill(psteps, 2, lens=[4096], with_state=False)
+        pre4k = bench_prefill(psteps, pwarm, lens=[4096], with_state=False)
         log(f"prefill 1x4096: {pre4k['ms'] * 1e3:.1f} us/step {pre4k['tflops']:.1f} TFLOP/s")
-    cpu = None
+    cpu = cpu_more = None
     if not args.no_cpu:
-        log("cpu baseline (decode B=64, fp32 C oracle)")
+        log("cpu baselines (fp32 C oracle): decode B=64, decode B=1, prefill 16x varlen")
         cpu = cpu_baseline_decode(budget_s=args.cpu_budget)
-        log(f"cpu: {cpu['value']:.2f} GB/s on {cpu['cores']} cores")
+        cpu1 = cpu_baseline_decode(batch=1, budget_s=2.0)
+        cpu1.update(value=cpu1["us_per_step"], unit="us/step (lower is better)")
+        cpu_more = {"decode_b1": cpu1}
+        if not args.no_prefill:
+            cpu_more["prefill"] = cpu_baseline_prefill(budget_s=args.cpu_budget)
+        log(f"cpu: {cpu['value']:.2f} GB/s on {cpu['cores']} of {cpu['cores_host']} cores")
     traffic = _traffic_from_profile("decode_b64_traffic.txt")
     rec = {
         "metric": METRIC,
@@ -236,25 +314,37 @@ def main():
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_more": cpu_more,
+        "decode_b1": {
+            "workload": "GDN decode, 1 sequence x 1 token (16 rotating buffer sets)",
+            "us_per_step": round(dec1["ms"] * 1e3, 2),
+            "gb_per_s": round(dec1["gbs"], 1),
+        },
+        "decode_b256_inplace": {
+            "workload": "GDN decode, 256 sequences x 1 token, new_state is state (2 sets)",
+            "us_per_step": round(dec256["ms"] * 1e3, 2),
+            "gb_per_s": round(dec256["gbs"], 1),
+            "hbm_frac": round(dec256["gbs"] / HBM_PEAK_GBS, 4),
+        },
     }
     if pre is not None:
-        rec["prefill_single_4k"] = {
-            "workload": "GDN prefill, 1 sequence x 4096 tokens, zero initial state",
-            "us_per_step": round(pre4k["ms"] * 1e3, 2),
-            "mtok_per_s": round(pre4k["mtok_s"], 2),
-            "tflops": round(pre4k["tflops"], 2),
-            "mfma_frac": round(pre4k["mfma_frac"], 4),
-        }
-        rec["prefill"] = {
-            "workload": f"GDN prefill, {pre['nseqs']} sequences, lengths ~U[64,1024] (seed 0), "
-                        f"T={pre['tokens']} tokens, non-zero fp32 initial state",
-            "us_per_step": round(pre["ms"] * 1e3, 2),
-            "mtok_per_s": round(pre["mtok_s"], 2),
-            "tflops": round(pre["tflops"], 2),
-            "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
-                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(pre["mfma_frac"], 4)},
-        }
+        for key, r, wl, st in (("prefill_single_4k", pre4k, "GDN prefill, 1 sequence x 4096 "
+                                "tokens, zero initial state", False),
+                               ("prefill", pre, f"GDN prefill, {pre['nseqs']} sequences, lengths "
+                                f"~U[64,1024] (seed 0), T={pre['tokens']} tokens, non-zero fp32 "
+                                "initial state", True)):
+            hbm = prefill_bytes(r["tokens"], r["nseqs"], with_state=st) / (r["ms"] * 1e-3) / 1e9
+            rec[key] = {
+                "workload": wl,
+                "us_per_step": round(r["ms"] * 1e3, 2),
+                "mtok_per_s": round(r["mtok_s"], 2),
+                "tflops": round(r["tflops"], 2),
+                "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
+                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(r["mfma_frac"], 4)},
+                "hbm_gb_per_s": round(hbm, 1),
+                "hbm_frac": round(hbm / HBM_PEAK_GBS, 4),
+            }
     print(json.dumps(rec), flush=True)
 
 

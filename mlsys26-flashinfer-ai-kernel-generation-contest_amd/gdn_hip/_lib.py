@@ -13,7 +13,7 @@ import threading
 
 import torch  # noqa: F401  (must precede CDLL: see module docstring)
 
-from .build import LIB_PATH
+from .build import FAST_NAME, LIB_PATH, fast_lib_path
 
 _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -125,6 +125,36 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(f"libgdn_hip.so ABI {ver} != binding ABI {ABI_VERSION}")
         _lib = lib
         return lib
+
+
+_fast = None
+_fast_tried = False
+
+
+def fast():
+    """The per-call fast path module (csrc/gdn_fast_path.cpp), initialised with this
+    library's entry points; None when it is not built (the Python path then validates
+    and marshals every call itself)."""
+    global _fast, _fast_tried
+    if _fast_tried:
+        return _fast
+    lib = load()  # takes _lock itself: before, not inside, the block below
+    with _lock:
+        if not _fast_tried:
+            path = fast_lib_path()
+            if path is not None:
+                import importlib.machinery
+                import importlib.util
+
+                loader = importlib.machinery.ExtensionFileLoader(FAST_NAME, path)
+                spec = importlib.util.spec_from_loader(FAST_NAME, loader)
+                mod = importlib.util.module_from_spec(spec)
+                loader.exec_module(mod)
+                addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
+                mod.init(addr(lib.gdn_decode_launch), addr(lib.gdn_last_error))
+                _fast = mod
+            _fast_tried = True
+    return _fast
 
 
 def last_error() -> str:

@@ -185,7 +185,6 @@ def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_sta
     return P, output, new_state, copy_back, keep
 
 
-@torch.no_grad()
 def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale, output=None, new_state=None):
     """Gated DeltaNet decode (k-last fp32 state).
 
@@ -198,17 +197,27 @@ def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale, output=None, new_sta
     (gdn_decode/solution/triton/kernel.py:117-118,146-147); new_state is the last token's
     update (the reference lets every token store it, in no fixed order).
     Mirrors gdn_decode/solution/triton/kernel.py:221-272 (defaults at :238-247).
+    Destination-passing calls (output and new_state given) whose buffers the kernel can
+    use in place are validated and launched by the C++ fast path; every other call goes
+    through the Python validation below, which raises the wrapper's errors.
     """
-    P, output, new_state, copy_back, _keep = _decode_marshal(
-        q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state)
-    if P.batch == 0:
-        return output, new_state
-    dev = q.device
-    lib = _lib.load()
-    with torch.cuda.device(dev):
-        _lib.check(lib.gdn_decode_launch(ctypes.byref(P), _stream(dev)), "gdn_decode_launch")
-    for user, tmp in copy_back:
-        user.copy_(tmp)
+    if output is not None and new_state is not None and (scale is None or type(scale) is float):
+        fast = _lib.fast()
+        if fast is not None and fast.decode(q, k, v, state, A_log, a, dt_bias, b,
+                                            0.0 if scale is None else scale, output,
+                                            new_state, _decode_variant) == 0:
+            return output, new_state
+    with torch.no_grad():
+        P, output, new_state, copy_back, _keep = _decode_marshal(
+            q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state)
+        if P.batch == 0:
+            return output, new_state
+        dev = q.device
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            _lib.check(lib.gdn_decode_launch(ctypes.byref(P), _stream(dev)), "gdn_decode_launch")
+        for user, tmp in copy_back:
+            user.copy_(tmp)
     return output, new_state
 
 

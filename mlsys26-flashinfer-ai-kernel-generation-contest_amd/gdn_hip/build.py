@@ -1,7 +1,10 @@
-"""Compile the HIP kernels (csrc/*.hip) into gdn_hip/libgdn_hip.so for gfx950.
+"""Compile the HIP kernels (csrc/*.hip) into gdn_hip/libgdn_hip.so for gfx950, and
+the host-only fast path of the Python entry points (csrc/gdn_fast_path.cpp) into
+gdn_hip/_fast/gdn_fast*.so.
 
-Plain hipcc, no torch extension machinery: the library exposes only the C ABI
-declared in include/gdn_hip.h and is loaded with ctypes.
+The kernels are plain hipcc with no torch extension machinery: the library exposes
+only the C ABI declared in include/gdn_hip.h and is loaded with ctypes. The fast path
+is a torch C++ extension (g++, torch headers) that calls that ABI.
 """
 from __future__ import annotations
 
@@ -18,6 +21,8 @@ CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = next((d for d in (os.path.join(REPO, "include"), os.path.join(ROOT, "include"))
                 if os.path.exists(os.path.join(d, "gdn_hip.h"))), os.path.join(REPO, "include"))
 LIB_PATH = os.path.join(PKG_DIR, "libgdn_hip.so")
+FAST_DIR = os.path.join(PKG_DIR, "_fast")
+FAST_NAME = "gdn_fast"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_*_f32).
@@ -57,5 +62,41 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+def fast_lib_path():
+    """Path of the built fast-path extension (None if not built)."""
+    import importlib.machinery
+
+    for suf in importlib.machinery.EXTENSION_SUFFIXES:
+        p = os.path.join(FAST_DIR, FAST_NAME + suf)
+        if os.path.exists(p):
+            return p
+    return None
+
+
+def build_fast(verbose: bool = False) -> str:
+    """Compile csrc/gdn_fast_path.cpp with torch's extension builder (host C++ only)."""
+    import torch
+    from torch.utils.cpp_extension import load
+
+    os.makedirs(FAST_DIR, exist_ok=True)
+    for f in glob.glob(os.path.join(FAST_DIR, "*.o")) + glob.glob(os.path.join(FAST_DIR, "*.so")):
+        os.remove(f)  # compile every time, like the HIP library
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    load(FAST_NAME, [os.path.join(CSRC, "gdn_fast_path.cpp")], build_directory=FAST_DIR,
+         extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1"],
+         extra_include_paths=["/opt/rocm/include", INCLUDE],
+         extra_ldflags=[f"-L{torch_lib}", "-lc10_hip"], verbose=verbose)
+    path = fast_lib_path()
+    if path is None:
+        raise RuntimeError(f"fast-path extension not found in {FAST_DIR} after building")
+    return path
+
+
+def build_all(verbose: bool = False) -> None:
+    build(verbose=verbose)
+    build_fast(verbose=verbose)
+
+
 if __name__ == "__main__":
-    print(build(verbose=True))
+    build_all(verbose=True)
+    print(LIB_PATH)

@@ -31,7 +31,7 @@ def _sources(solution_dir):
     files = [(os.path.join(solution_dir, "kernel.py"), "kernel.py")]
     for f in sorted(glob.glob(os.path.join(PKG_DIR, "*.py"))):
         files.append((f, "gdn_hip/" + os.path.basename(f)))
-    for pat in ("*.hip", "*.h"):
+    for pat in ("*.hip", "*.h", "*.cpp"):
         for f in sorted(glob.glob(os.path.join(ROOT, "csrc", pat))):
             files.append((f, "csrc/" + os.path.basename(f)))
     files.append((os.path.join(REPO, "include", "gdn_hip.h"), "include/gdn_hip.h"))

@@ -147,3 +147,28 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(L, "LIB_PATH", str(tmp_path / "absent.so"))
     with pytest.raises(RuntimeError, match="not built"):
         L.load()
+
+
+def test_fast_path_extension_loads_and_declines_host_tensors():
+    """The C++ per-call fast path loads next to the library (from any thread, without
+    deadlocking on the loader's lock) and declines tensors that are not on a HIP device,
+    which the Python path then rejects."""
+    import threading
+
+    import torch
+
+    from gdn_hip import _lib
+
+    res = []
+    th = threading.Thread(target=lambda: res.append(_lib.fast()))
+    th.start()
+    th.join(timeout=60)
+    assert not th.is_alive(), "loading the fast path hung"
+    fast = res[0]
+    assert fast is not None, "fast-path extension not built (gdn_hip.build.build_fast)"
+    assert _lib.fast() is fast
+    t = lambda *s: torch.zeros(s, dtype=torch.bfloat16)  # noqa: E731
+    f = lambda *s: torch.zeros(s, dtype=torch.float32)  # noqa: E731
+    assert fast.decode(t(1, 1, 4, 128), t(1, 1, 4, 128), t(1, 1, 8, 128), f(1, 8, 128, 128),
+                       f(8), t(1, 1, 8), f(8), t(1, 1, 8), 0.5, t(1, 1, 8, 128),
+                       f(1, 8, 128, 128), 0) == 1

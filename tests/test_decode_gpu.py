@@ -304,3 +304,61 @@ def test_decode_plan_in_graph(dev):
         torch.cuda.synchronize()
         assert torch.equal(out, eager_out), f"replay {r}: output differs"
         assert torch.equal(ns, eager_ns), f"replay {r}: new_state differs"
+
+
+def test_decode_fast_path_taken_and_exact(dev):
+    """A destination-passing call with in-place-usable buffers goes through the C++ fast
+    path (validation and marshalling in C++): it launches (returns 0), matches the oracle
+    and equals the Python path's result bit for bit."""
+    from gdn_hip import _lib
+    from gdn_hip.api import _decode_marshal
+
+    fast = _lib.fast()
+    assert fast is not None, "fast-path extension not built (gdn_hip.build.build_fast)"
+    inp = decode_inputs(16, hqk=4, hv=8, seed=77)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out, ns = torch.empty_like(g.v), torch.empty_like(g.state)
+    assert fast.decode(*g.args(), out, ns, 0) == 0
+    torch.cuda.synchronize()
+    _check(out, ns, ref_out, ref_ns, "fast path")
+    # the Python path (ctypes) on the same inputs
+    P, o2, n2, copy_back, keep = _decode_marshal(*g.args(), torch.empty_like(out),
+                                                 torch.empty_like(ns))
+    import ctypes
+    _lib.check(_lib.load().gdn_decode_launch(ctypes.byref(P), ctypes.c_void_p(
+        torch.cuda.current_stream(dev).cuda_stream)), "gdn_decode_launch")
+    torch.cuda.synchronize()
+    assert torch.equal(out, o2) and torch.equal(ns, n2)
+
+
+def test_decode_fast_path_declines_what_it_cannot_use(dev):
+    """Calls the fast path cannot serve in place return 1 (the general path then handles
+    them): a non-unit inner stride, a CPU tensor, a wrong dtype, mismatched shapes and an
+    in-place state with a token axis. The public entry point still serves the strided
+    output correctly."""
+    from gdn_hip import _lib
+
+    fast = _lib.fast()
+    inp = decode_inputs(4, seed=5)
+    g = inp.to(dev)
+    out, ns = torch.empty_like(g.v), torch.empty_like(g.state)
+    a = list(g.args())
+    wide = torch.empty((4, 1, 32, 256), dtype=torch.bfloat16, device=dev)
+    assert fast.decode(*a, wide[..., ::2], ns, 0) == 1
+    a_cpu = list(a)
+    a_cpu[0] = a[0].cpu()
+    assert fast.decode(*a_cpu, out, ns, 0) == 1
+    a_dt = list(a)
+    a_dt[4] = a[4].double()
+    assert fast.decode(*a_dt, out, ns, 0) == 1
+    assert fast.decode(*a, out, ns[:2], 0) == 1
+    t2 = decode_inputs(3, seed=6, seq_len=2).to(dev)
+    st = t2.state.clone()
+    args2 = list(t2.args())
+    args2[3] = st
+    assert fast.decode(*args2, torch.empty_like(t2.v), st, 0) == 1
+    ref_out, ref_ns = _oracle(inp)
+    o, s = gdn_decode(*g.args(), wide[..., ::2], ns)
+    torch.cuda.synchronize()
+    _check(o, s, ref_out, ref_ns, "general path via strided output")
