@@ -128,6 +128,21 @@ int64_t gdn_prefill_workspace_size(int32_t total_tokens, int32_t num_seqs,
 
 int gdn_prefill_launch(const gdn_prefill_params *p, void *stream);
 
+/*
+ * gdn_prefill_launch without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference, which keeps its prefill state in registers.
+ * The workspace is a static device array of gdn_prefill_noalloc_capacity() bytes
+ * (96 MiB) per device, set up on the first call on that device and held until the
+ * process ends; p->workspace and p->workspace_bytes are ignored. Sizes whose
+ * gdn_prefill_workspace_size exceeds it fail with GDN_EWORKSPACE before any launch
+ * (at 32 v-heads: about 11,000 tokens in 16 sequences). Calls on one device share the
+ * array: calls that overlap in time on one device (other streams, unordered host
+ * threads) race. Nothing is allocated, freed or memset.
+ */
+int64_t gdn_prefill_noalloc_capacity(void);
+int gdn_prefill_launch_noalloc(const gdn_prefill_params *p, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -91,6 +91,8 @@ EXPORTED = (
     "gdn_decode_launch",
     "gdn_prefill_workspace_size",
     "gdn_prefill_launch",
+    "gdn_prefill_noalloc_capacity",
+    "gdn_prefill_launch_noalloc",
 )
 
 _lib = None
@@ -120,6 +122,10 @@ def load() -> ctypes.CDLL:
         lib.gdn_prefill_workspace_size.argtypes = [_c_i32] * 5
         lib.gdn_prefill_launch.restype = ctypes.c_int
         lib.gdn_prefill_launch.argtypes = [ctypes.POINTER(PrefillParams), _c_ptr]
+        lib.gdn_prefill_noalloc_capacity.restype = _c_i64
+        lib.gdn_prefill_noalloc_capacity.argtypes = []
+        lib.gdn_prefill_launch_noalloc.restype = ctypes.c_int
+        lib.gdn_prefill_launch_noalloc.argtypes = [ctypes.POINTER(PrefillParams), _c_ptr]
         ver = lib.gdn_abi_version()
         if ver != ABI_VERSION:
             raise RuntimeError(f"libgdn_hip.so ABI {ver} != binding ABI {ABI_VERSION}")
