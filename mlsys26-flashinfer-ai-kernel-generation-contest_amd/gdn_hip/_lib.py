@@ -157,7 +157,8 @@ def fast():
                 mod = importlib.util.module_from_spec(spec)
                 loader.exec_module(mod)
                 addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
-                mod.init(addr(lib.gdn_decode_launch), addr(lib.gdn_last_error))
+                mod.init(addr(lib.gdn_decode_launch), addr(lib.gdn_prefill_launch),
+                         addr(lib.gdn_prefill_workspace_size), addr(lib.gdn_last_error))
                 _fast = mod
             _fast_tried = True
     return _fast

@@ -236,12 +236,13 @@ class DecodePlan:
                                                                   dt_bias, b))):
             raise ValueError("DecodePlan needs buffers the kernel can use in place")
         self._P, self._keep, self.output, self.new_state = P, keep, out, ns
-        self._dev = q.device
-        self._lib = _lib.load()
+        self._pref = ctypes.byref(P)
+        self._dev_index = q.device.index
+        self._launch = _lib.load().gdn_decode_launch
 
     def run(self):
-        _lib.check(self._lib.gdn_decode_launch(ctypes.byref(self._P), _stream(self._dev)),
-                   "gdn_decode_launch")
+        stream = torch._C._cuda_getCurrentRawStream(self._dev_index)
+        _lib.check(self._launch(self._pref, stream), "gdn_decode_launch")
         return self.output, self.new_state
 
 
@@ -292,11 +293,14 @@ def _workspace(dev, stream, nbytes):
 
 
 def release_workspace() -> None:
-    """Drop the cached eager prefill workspaces (they return to torch's caching
-    allocator once in-flight calls on their streams are done with them: the caller
-    synchronises first). Workspaces of captured graphs are kept."""
+    """Drop the cached eager prefill workspaces, the Python path's and the fast path's
+    (they return to torch's caching allocator; the caller synchronises first, so that no
+    call in flight still uses them). Workspaces of captured graphs are kept."""
     with _ws_lock:
         _ws_cache.clear()
+    fast = _lib.fast()
+    if fast is not None:
+        fast.release_workspace()
 
 
 def _prefill_marshal(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
@@ -405,7 +409,6 @@ def _prefill_marshal(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, ou
     return P, output, new_state, copy_back, keep, stream
 
 
-@torch.no_grad()
 def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=None,
                 new_state=None):
     """Gated DeltaNet prefill over packed variable-length sequences.
@@ -417,16 +420,26 @@ def gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output=
     Mirrors gdn_prefill/solution/triton/kernel.py:253-337 (argument order :254,
     defaults and DPS handling :276-302), generalised from the 4/8 head layout it
     asserts (:271-274) to any HV that is a multiple of HQK.
+    Destination-passing calls outside graph capture whose buffers the kernels can use in
+    place are validated and launched by the C++ fast path (with its own per-stream
+    workspace cache); every other call goes through the Python validation below.
     """
-    m = _prefill_marshal(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
-                         new_state)
-    if len(m) == 1:  # nothing to launch
-        return m[0]
-    P, output, new_state, copy_back, _keep, stream = m
-    with torch.cuda.device(q.device):
-        _lib.check(_lib.load().gdn_prefill_launch(ctypes.byref(P),
-                                                  ctypes.c_void_p(stream.cuda_stream)),
-                   "gdn_prefill_launch")
-    for user, tmp in copy_back:
-        user.copy_(tmp)
+    if output is not None and new_state is not None and (scale is None or type(scale) is float):
+        fast = _lib.fast()
+        if fast is not None and fast.prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                                             0.0 if scale is None else scale, output,
+                                             new_state, _prefill_variant) == 0:
+            return output, new_state
+    with torch.no_grad():
+        m = _prefill_marshal(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                             new_state)
+        if len(m) == 1:  # nothing to launch
+            return m[0]
+        P, output, new_state, copy_back, _keep, stream = m
+        with torch.cuda.device(q.device):
+            _lib.check(_lib.load().gdn_prefill_launch(ctypes.byref(P),
+                                                      ctypes.c_void_p(stream.cuda_stream)),
+                       "gdn_prefill_launch")
+        for user, tmp in copy_back:
+            user.copy_(tmp)
     return output, new_state

@@ -424,3 +424,65 @@ def test_prefill_graphs_keep_their_own_workspaces(dev):
         print(f"[two graphs] replay {r} bitwise: {torch.equal(o, eo)} {torch.equal(n, en)}",
               flush=True)
         assert torch.equal(o, eo) and torch.equal(n, en), f"replay {r} differs"
+
+
+def test_prefill_fast_path_taken_and_exact(dev):
+    """A destination-passing prefill outside capture goes through the C++ fast path: it
+    launches (returns 0), matches the oracle and equals the Python path bit for bit; after
+    release_workspace() it allocates a fresh workspace and still matches."""
+    from gdn_hip import _lib
+    from gdn_hip.api import release_workspace
+
+    fast = _lib.fast()
+    assert fast is not None
+    inp = prefill_inputs([300, 64, 129, 1], hqk=4, hv=8, seed=88, with_state=True)
+    ref_o, ref_s = _oracle(inp)
+    g = inp.to(dev)
+    T, N = g.q.shape[0], len(inp.seqlens)
+    out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+    assert fast.prefill(*g.args(), out, ns, 0) == 0
+    torch.cuda.synchronize()
+    _check(out, ns, ref_o, ref_s, "prefill fast path")
+    import ctypes
+
+    from gdn_hip.api import _prefill_marshal
+    o2, n2 = torch.empty_like(out), torch.empty_like(ns)
+    P, _, _, copy_back, keep, stream = _prefill_marshal(*g.args(), o2, n2)
+    assert not copy_back
+    _lib.check(_lib.load().gdn_prefill_launch(ctypes.byref(P), ctypes.c_void_p(
+        stream.cuda_stream)), "gdn_prefill_launch")
+    torch.cuda.synchronize()
+    assert torch.equal(out, o2) and torch.equal(ns, n2)
+    release_workspace()
+    o3, n3 = gdn_prefill(*g.args(), torch.empty_like(out), torch.empty_like(ns))
+    torch.cuda.synchronize()
+    assert torch.equal(out, o3) and torch.equal(ns, n3)
+
+
+def test_prefill_fast_path_declines_capture_and_odd_layouts(dev):
+    """Graph capture, a strided output and empty inputs go to the general path."""
+    from gdn_hip import _lib
+
+    fast = _lib.fast()
+    g = prefill_inputs([70, 30], seed=89, with_state=True).to(dev)
+    T = g.q.shape[0]
+    out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((2, 32, 128, 128), dtype=torch.float32, device=dev)
+    wide = torch.empty((T, 32, 256), dtype=torch.bfloat16, device=dev)
+    assert fast.prefill(*g.args(), wide[..., ::2], ns, 0) == 1
+    e = prefill_inputs([0, 0], seed=2, with_state=True).to(dev)
+    assert fast.prefill(*e.args(), torch.empty((0, 32, 128), dtype=torch.bfloat16, device=dev),
+                        torch.empty_like(e.state), 0) == 1
+    fast.prefill(*g.args(), out, ns, 0)  # warm the stream's cached workspace
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        gdn_prefill(*g.args(), output=out, new_state=ns)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = fast.prefill(*g.args(), out, ns, 0)
+    assert rc == 1
