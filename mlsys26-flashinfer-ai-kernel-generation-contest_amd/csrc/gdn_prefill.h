@@ -278,6 +278,12 @@ struct ScanArgs {
     const int32_t *jobs;
     int job_first, njob_idx;
     float *seg_sin, *seg_r, *seg_mt;
+    // Fused kernel only (prep waves build each chunk's T', P' and gates in LDS): the gate
+    // inputs and the readout scale.
+    const bf16_t *a, *b;
+    const float *A_log, *dt_bias;
+    int64_t a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
+    float scale;
 };
 
 
@@ -332,6 +338,32 @@ constexpr bool layouts_invert()
 }
 static_assert(layouts_invert(), "T' / P' LDS layouts must be bijections");
 
+// Row order inside a 16-row block used for fp32 MFMA operands: pi(m) = 4 (m % 4) + m / 4
+// (a 4 x 4 transpose, its own inverse). With pi-ordered rows an MFMA result in C layout
+// (lane (n, g) holds rows 4 g + i) already holds rows 4 i + g: exactly the operand
+// layout of the next v_mfma_f32_16x16x4_f32 (k-slice i, lane (n, g) supplies k = 4 i + g).
+__device__ __forceinline__ int pi16(int m) { return 4 * (m & 3) + (m >> 2); }
+
+// acc += coef * (acc of lane K in this 16-lane row): one v_fmac_f32 with a DPP row_newbcast
+// source. Callers keep >= 2 other VALU instructions between the last write of acc and
+// this read (the DPP read-after-write hazard); the first use in a chain is preceded by
+// s_nop 1.
+#define GDN_FMAC_BCAST(acc, coef, K)                                                     \
+    asm volatile("v_fmac_f32_dpp %0, %0, %1 row_newbcast:" #K " row_mask:0xf bank_mask:0xf" \
+                 : "+v"(acc)                                                              \
+                 : "v"(coef))
+
+// One chunk in LDS, as the workgroup's waves read it.
+template <int NW>
+struct ScanBuf {
+    u32x4 K[kC * 16];      // 16 KB
+    u32x4 Q[kC * 16];      // 16 KB
+    u32x4 V[kC * 2 * NW];  // the workgroup's 16 NW value columns
+    u32x4 T[2][512];       // T' hi / lo (tlay)
+    u32x4 P[512];          // P' (play)
+    f32x4 G[64];           // the record's gate area (gamma, dec, scale gamma, gammaC)
+};
+
 // ------------------------------------------------------------------------- kernels
 // Defined in gdn_prefill_plan.hip, gdn_prefill_prep.hip and gdn_prefill_scan.hip; the
 // scan kernels are instantiated there for SEG = false (whole sequences) and true
@@ -343,6 +375,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void
 gdn_prefill_prep2_kernel(PrepArgs p);
 template <bool SEG>
 __global__ __launch_bounds__(512) void gdn_prefill_scan8_kernel(ScanArgs p);
+// Whole sequences without a prep pass: 8 scan waves and 4 prep waves per workgroup; the prep
+// waves build chunk c + 1's T', P' and gates in LDS while the scan waves process chunk c.
+__global__ __launch_bounds__(768) void gdn_prefill_fused_kernel(ScanArgs p);
 template <bool SEG>
 __global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p);
 

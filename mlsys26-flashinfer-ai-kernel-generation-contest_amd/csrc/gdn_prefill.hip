@@ -200,6 +200,14 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     pa.o_sh = p->output_stride[1];
     // segments only for the default variant (the tuning variants keep whole sequences)
     const int G = p->variant == 0 ? L.G : 1;
+    // Whole sequences: 4 scan waves per workgroup (two workgroups per (sequence, v-head))
+    // when there are at most 128 (sequence, v-head) pairs, else 8. Variants: 1 forces 4
+    // waves, 2 forces 8, 3 runs the fused kernel (8 scan waves and 4 prep waves, no prep
+    // pass and no records). The fused kernel is exact but slower on MI355X: the prep
+    // waves' per-chunk chain (copies, gates, P' and A, substitution, T chain, ~12k cycles)
+    // outlasts a scan chunk (~6.7k), so the scan waves wait for it at every chunk.
+    const bool nw4 = p->variant == 1 || (p->variant == 0 && (int64_t)N * HV <= 128);
+    const bool fused = G == 1 && p->variant == 3;
     pa.seg_G = G;
     pa.seg_capA = (int)L.capA;
     pa.jobs = G > 1 ? (int32_t *)(ws + L.jobs) : nullptr;
@@ -210,7 +218,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     if (rc)
         return rc;
 
-    if (L.nc > 0 && T > 0) {
+    if (L.nc > 0 && T > 0 && !fused) {
         gdn::PrepArgs qa;
         qa.q = (const gdn::bf16_t *)p->q;
         qa.k = (const gdn::bf16_t *)p->k;
@@ -290,6 +298,17 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         sa.seg_sin = G > 1 ? (float *)(ws + L.seg_sin) : nullptr;
         sa.seg_r = G > 1 ? (float *)(ws + L.seg_r) : nullptr;
         sa.seg_mt = G > 1 ? (float *)(ws + L.seg_mt) : nullptr;
+        sa.a = (const gdn::bf16_t *)p->a;
+        sa.b = (const gdn::bf16_t *)p->b;
+        sa.A_log = p->A_log;
+        sa.dt_bias = p->dt_bias;
+        sa.a_st = p->a_stride[0];
+        sa.a_sh = p->a_stride[1];
+        sa.b_st = p->b_stride[0];
+        sa.b_sh = p->b_stride[1];
+        sa.A_log_s = p->A_log_stride;
+        sa.dt_s = p->dt_bias_stride;
+        sa.scale = p->scale;
         // 8 waves per workgroup = one (sequence, v-head) each, two waves per SIMD; with
         // few (sequence, v-head) pairs, 4 waves and two workgroups per pair spread the
         // state rows over twice as many CUs. variant: 1 forces 4 waves, 2 forces 8.
@@ -301,7 +320,9 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
             if (ngroups > 0x7fffffff || blocks > 0x7fffffff)
                 return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
             const dim3 grid((unsigned)blocks), b4(256), b8(512);
-            if (sa.jobs && nw4)
+            if (fused && !sa.jobs)
+                hipLaunchKernelGGL(gdn::gdn_prefill_fused_kernel, grid, dim3(768), 0, st, sa);
+            else if (sa.jobs && nw4)
                 hipLaunchKernelGGL(gdn::gdn_prefill_scan4_kernel<true>, grid, b4, 0, st, sa);
             else if (sa.jobs)
                 hipLaunchKernelGGL(gdn::gdn_prefill_scan8_kernel<true>, grid, b8, 0, st, sa);
@@ -325,7 +346,6 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
             sa.njob_idx = 2;
             rc = scan(L.capC, L.capC * HV <= 128);
         } else {
-            const bool nw4 = p->variant == 1 || (p->variant != 2 && (int64_t)N * HV <= 128);
             rc = scan(N, nw4);
         }
         if (rc)

@@ -4,21 +4,6 @@
 
 namespace gdn {
 
-// Row order inside a 16-row block used for fp32 MFMA operands: pi(m) = 4 (m % 4) + m / 4
-// (a 4 x 4 transpose, its own inverse). With pi-ordered rows an MFMA result in C layout
-// (lane (n, g) holds rows 4 g + i) already holds rows 4 i + g: exactly the operand
-// layout of the next v_mfma_f32_16x16x4_f32 (k-slice i, lane (n, g) supplies k = 4 i + g).
-__device__ __forceinline__ int pi16(int m) { return 4 * (m & 3) + (m >> 2); }
-
-// acc += coef * (acc of lane K in this 16-lane row): one v_fmac_f32 with a DPP row_newbcast
-// source. Callers keep >= 2 other VALU instructions between the last write of acc and
-// this read (the DPP read-after-write hazard); the first use in a chain is preceded by
-// s_nop 1.
-#define GDN_FMAC_BCAST(acc, coef, K)                                                     \
-    asm volatile("v_fmac_f32_dpp %0, %0, %1 row_newbcast:" #K " row_mask:0xf bank_mask:0xf" \
-                 : "+v"(acc)                                                              \
-                 : "v"(coef))
-
 // Work unit: (chunk, q/k head, group of VH v-heads). A persistent workgroup of 4 VH waves
 // walks units u = blockIdx.x, + gridDim.x, ...; wave (hv, w) = v-head hv of the group,
 // block w. The unit's K and Q go to LDS once (direct copies; K double-buffered, the next
@@ -267,7 +252,9 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2)
                 x[s2] = pi16(lr) == lg + 4 * s2 ? 1.f : 0.f;
-            asm volatile("s_nop 1" ::: "memory");
+            // x enters the asm, so its initialisation is done before the nop: the first DPP
+        // read of each x[s2] then has the two wait states a VALU write needs before it
+        asm volatile("s_nop 1" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]) : : "memory");
             // arow holds -A; the broadcast lane of step M is pi(M)
 #define GDN_SUBST_STEP(M, K)                                                      \
             GDN_FMAC_BCAST(x[0], arow[M], K); GDN_FMAC_BCAST(x[1], arow[M], K);   \

@@ -1,19 +1,9 @@
 // Prefill scan kernels: the sequential chunk recurrence, state in registers, for whole
 // sequences or segment jobs.
 #include "gdn_prefill.h"
+#include "gdn_prefill_fused_prep.h"
 
 namespace gdn {
-
-// One chunk in LDS, as the workgroup's waves read it.
-template <int NW>
-struct ScanBuf {
-    u32x4 K[kC * 16];      // 16 KB
-    u32x4 Q[kC * 16];      // 16 KB
-    u32x4 V[kC * 2 * NW];  // the workgroup's 16 NW value columns
-    u32x4 T[2][512];       // T' hi / lo (tlay)
-    u32x4 P[512];          // P' (play)
-    f32x4 G[64];           // the record's gate area (gamma, dec, scale gamma, gammaC)
-};
 
 // Copy windows of one chunk, 64 units (1 KB) each: K rows 4b..4b+3 (16 windows), Q (16),
 // V (NW == 8: 4 rows per window, NW == 4: 8 rows), then 6 windows each of T' hi, T' lo
@@ -36,9 +26,14 @@ struct ScanBuf {
 // V columns are read with the LDS transpose read.
 // SEG: the grid walks segment jobs (p.jobs); otherwise whole sequences, and none of the
 // segment code is compiled in (it costs the whole-sequence loop registers).
-template <int NW, bool SEG>
-__device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, ScanBuf<NW> &BB)
+// FUSED (NW == 8, whole sequences): the workgroup has 4 more waves, the prep waves, which
+// build chunk c + 1's K, Q (copies), T', P' and gate area in the other chunk buffer while
+// the 8 scan waves process chunk c; the scan waves copy only V. No records are read.
+template <int NW, bool SEG, bool FUSED = false>
+__device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, ScanBuf<NW> &BB,
+                                          FusedPrepScratch *ps = nullptr)
 {
+    static_assert(!FUSED || (NW == 8 && !SEG), "the fused kernel scans whole sequences, 8 waves");
     constexpr int TPH = 8 / NW;  // workgroups per (sequence, v-head)
     // Workgroups of one (sequence, q/k head) share K, Q through L2: one XCD for them all
     // (workgroup ids are dealt to the 8 XCDs round-robin).
@@ -78,6 +73,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
               lr = l & 15, lg = l >> 4;
     const int v0w = v0 + 16 * w;
+    const bool prepw = FUSED && w >= NW;  // a prep wave (wave-uniform)
+    const int pw = w - NW;                // its column block
 
     // ---- copy plan. Every copy is a buffer load straight to LDS; per-lane source offsets
     // are chunk-invariant and computed once. Rows past a chunk's end fall outside the
@@ -96,14 +93,33 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
 
     constexpr int VWIN = 2 * NW;               // V windows
     constexpr int NWIN = 32 + VWIN + 19;       // all windows
-    constexpr int PER = (NWIN + NW - 1) / NW;  // windows per wave
+    // windows per wave (fused: scan waves copy 2 V windows, prep waves 8 K / Q windows)
+    constexpr int PER = FUSED ? 2 : (NWIN + NW - 1) / NW;
+    constexpr int PERP = 8;
 
     // Source offset of this lane in window i (compile-time) of this wave; window kinds
     // follow win = w + NW i: K rows 4b..4b+3 (16 windows), Q (16), V (NW == 8: 4 rows per
     // window, NW == 4: 8 rows), then 18 T' / P' windows and the gate area.
-    uint32_t woff[PER];
+    uint32_t woff[FUSED ? PERP : PER];
+    if constexpr (FUSED) {
+#pragma unroll
+        for (int i = 0; i < PERP; ++i) {
+            uint32_t off;
+            if (prepw) {  // K windows pw + 4 i, then Q windows pw + 4 (i - 4)
+                const int t = 4 * (pw + 4 * (i & 3)) + (l >> 4), cs = l & 15;
+                off = i < 4 ? (uint32_t)t * kst2 + 16u * (cs ^ kswz(t))
+                            : (uint32_t)t * qst2 + 16u * (cs ^ (t & 15));
+            } else {  // V windows w + 8 i
+                const int t = 4 * (w + NW * (i & 1)) + (l >> 4), cs = l & 15;
+                off = (uint32_t)t * vst2 + 16u * (cs ^ (2 * (t & 3)));
+            }
+            woff[i] = off;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
+        if constexpr (FUSED)
+            break;
         const int win = w + NW * i;
         uint32_t off = 0;
         if (NW * i < 16) {
@@ -154,6 +170,10 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     auto chunk_src = [&](int c) { return chunk_src_v(c, true); };
     auto issue_win = [&](ScanBuf<NW> &B, const ChunkSrc &cs, const int i) {
         const int win = w + NW * i;  // window kind is a compile-time function of i
+        if constexpr (FUSED) {  // scan waves: V windows w + 8 i
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.v, (GDN_LDS void *)&B.V[64 * win], 16, woff[i], 0, 0, 0);
+            return;
+        }
         if (NW * i < 16) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.k, (GDN_LDS void *)&B.K[64 * win], 16, woff[i], 0, 0, 0);
         } else if (NW * i < 32) {
@@ -176,6 +196,18 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
 #pragma unroll
         for (int i = 0; i < PER; ++i)
             issue_win(B, cs, i);
+    };
+    // prep waves: chunk c's K and Q into B
+    auto issue_kq = [&](ScanBuf<NW> &B, int c) {
+        const ChunkSrc cs = chunk_src(c);
+#pragma unroll
+        for (int i = 0; i < PERP; ++i) {
+            const int b = pw + 4 * (i & 3);
+            if (i < 4)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.k, (GDN_LDS void *)&B.K[64 * b], 16, woff[i], 0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.q, (GDN_LDS void *)&B.Q[64 * b], 16, woff[i], 0, 0, 0);
+        }
     };
 
     // ---- LDS read offsets (bytes within a ScanBuf member; chunk-invariant)
@@ -220,7 +252,47 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         for (int t = 0; t < 8; ++t)
             R[t] = *(const f32x4 *)(rp + 256 * t);
     };
-    if (chain) {
+    // fused: the prep waves' meeting counter lives in the padding of buffer A's gate area
+    // (floats 193 .. 255 of it are never written or read otherwise)
+    int meet = 0;
+    int *const ctr = (int *)((float *)BA.G + 255);
+    auto prep_next = [&](ScanBuf<NW> &B, int c) {  // prep waves: chunk c into B
+        issue_kq(B, c);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's K / Q copies landed
+        meet += kPrepWaves;
+        prep_meet(ctr, meet);                // ... and every prep wave's
+        if constexpr (FUSED)
+            fused_prep_chunk(p, B, *ps, ctr, meet, pw, h, (int64_t)tok0 + (int64_t)c * kC,
+                             min(kC, len - c * kC));
+    };
+    if constexpr (FUSED) {
+        // T' / P' of both buffers start at zero: the prep waves write only the blocks on
+        // and below the diagonal, and the scan reads some units above it as zeros
+        u32x4 *za = &BA.T[0][0], *zb = &BB.T[0][0];
+        static_assert(sizeof(BA.T) + sizeof(BA.P) == 1536 * 16, "T' and P' are adjacent");
+        for (int u = tid; u < 1536; u += 64 * (NW + kPrepWaves)) {
+            za[u] = u32x4{0u, 0u, 0u, 0u};
+            zb[u] = u32x4{0u, 0u, 0u, 0u};
+        }
+        if (tid == 0)
+            *ctr = 0;
+        lds_barrier();
+        if (prepw) {
+            // the prep waves' own loop, with the scan loop's barriers: one per chunk, after
+            // which chunk c is ready in its buffer (chunk c in BA when c - cb is even)
+            __builtin_amdgcn_s_setprio(3);  // their chain gates every chunk: first pick
+            if (ce > cb)
+                prep_next(BA, cb);
+            for (int c = cb; c < ce; ++c) {
+                dma_barrier();
+                if (c + 1 < ce)
+                    prep_next(((c + 1 - cb) & 1) ? BB : BA, c + 1);
+            }
+            return;
+        }
+        if (ce > cb)
+            issue_chunk(BA, cb);
+    } else if (chain) {
         issue_m(q);
         load_r(q);
         // unconditional, so the number of operations in flight is the same on every path
@@ -321,20 +393,24 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
 
     // Operand reads run one step ahead of the MFMAs that consume them; sched_barrier
     // keeps each step's reads, VALU work and MFMAs in the order written.
-    // The next chunk's copies (PER windows) are spread over phases (a) and (c): issued
-    // all at once they queue behind each other and stall the issuing waves.
-    auto compute = [&](ScanBuf<NW> &B, int c, ScanBuf<NW> &Bn, bool more) {
-        const int lenc = min(kC, len - c * kC);
-        const ChunkSrc ncs = chunk_src(more ? c + 1 : c);
-        auto dma_at = [&](const int slot) {  // slots 0..7: after (a) steps 0..3, (c) tiles 0..3
+    // A chunk is two halves: phase1 = (a) X = K S0^T, (b) R = V - gamma X, (c) U = T' R;
+    // phase2 = (d) W = dec U, (e) the outputs, (f) the state update. The next chunk's
+    // copies (PER windows per wave) are spread over phase1: issued all at once they queue
+    // behind each other and stall the issuing waves.
+    u32x4 Bh[4];  // S0 hi, from phase1 (a) to phase2 (e)
+    f32x4 U[4];   // phase1 (c) -> phase2 (d)
+    f32x4 dc[4];  // the gate area's dec, read in phase1 (c) for phase2 (d)
+    auto issue_slot = [&](ScanBuf<NW> &Bn, const ChunkSrc &ncs, bool issue, const int slot) {
 #pragma unroll
-            for (int i = 0; i < PER; ++i)
-                if ((i * 8) / PER == slot && more)
-                    issue_win(Bn, ncs, i);
-        };
-        const char *Kb = (const char *)B.K, *Qb = (const char *)B.Q, *Vb = (const char *)B.V;
+        for (int i = 0; i < PER; ++i)  // slots 0..7
+            if ((i * 8) / PER == slot && issue)
+                issue_win(Bn, ncs, i);
+    };
+    // copies at slots 0..7: after (a) steps 0..3 and (c) tiles 0..3
+    auto phase1 = [&](ScanBuf<NW> &B, ScanBuf<NW> &Bn, const ChunkSrc &ncs, bool issue) {
+        const char *Kb = (const char *)B.K, *Vb = (const char *)B.V;
         const char *Th = (const char *)B.T[0], *Tl = (const char *)B.T[1];
-        const char *Pb = (const char *)B.P, *Gb = (const char *)B.G;
+        const char *Gb = (const char *)B.G;
         auto kA = [&](int s, int tt) {
             return *(const u32x4 *)(Kb + koffA[s] + 256 * (32 * (tt >> 1) + 4 * (tt & 1)));
         };
@@ -349,7 +425,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         };
 
         // (a) S0 as MFMA operands (hi + lo), X = K S0^T
-        u32x4 Bh[4], Bl[4], ka[2][4];
+        u32x4 Bl[4], ka[2][4];
         f32x4 X[4];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
@@ -382,7 +458,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 X[tt] = mfma_bf16(ka[s & 1][tt], Bh[s], X[tt]);
                 X[tt] = mfma_bf16(ka[s & 1][tt], Bl[s], X[tt]);
             }
-            dma_at(s);
+            issue_slot(Bn, ncs, issue, s);
         }
         __builtin_amdgcn_sched_barrier(0);
 
@@ -410,8 +486,6 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         }
 
         // (c) U = T' R
-        f32x4 U[4];
-        f32x4 dc[4];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
             __builtin_amdgcn_sched_barrier(0);
@@ -432,9 +506,15 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
                 U[tt] = mfma_bf16(tA[cb][sp][0], Rl[sp], U[tt]);
                 U[tt] = mfma_bf16(tA[cb][sp][1], Rh[sp], U[tt]);
             }
-            dma_at(4 + tt);
+            issue_slot(Bn, ncs, issue, 4 + tt);
         }
         __builtin_amdgcn_sched_barrier(0);
+    };
+
+    auto phase2 = [&](ScanBuf<NW> &B, int c) {
+        const int lenc = min(kC, len - c * kC);
+        const char *Kb = (const char *)B.K, *Qb = (const char *)B.Q;
+        const char *Pb = (const char *)B.P, *Gb = (const char *)B.G;
 
         // (d) W = dec U (hi + lo) for the state update, U (bf16) for the readout
         auto qRead = [&](int tt, u32x4 *qv, u32x4 *pv) {
@@ -530,6 +610,11 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         __builtin_amdgcn_sched_barrier(0);
     };
 
+    auto compute = [&](ScanBuf<NW> &B, int c, ScanBuf<NW> &Bn, bool more) {
+        const ChunkSrc ncs = chunk_src(more ? c + 1 : c);
+        phase1(B, Bn, ncs, more);
+        phase2(B, c);
+    };
     for (int c = cb; c < ce; c += 2) {
         dma_barrier();  // chunk c is in BA; every wave is done with BB
         compute(BA, c, BB, c + 1 < ce);
@@ -604,6 +689,13 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p)
 {
     __shared__ ScanBuf<4> bufA, bufB;
     scan_body<4, SEG>(p, bufA, bufB);
+}
+
+__global__ __launch_bounds__(768) void gdn_prefill_fused_kernel(ScanArgs p)
+{
+    __shared__ ScanBuf<8> bufA, bufB;
+    __shared__ FusedPrepScratch ps;
+    scan_body<8, false, true>(p, bufA, bufB, &ps);
 }
 
 template __global__ void gdn_prefill_scan8_kernel<false>(ScanArgs p);

@@ -486,3 +486,25 @@ def test_prefill_fast_path_declines_capture_and_odd_layouts(dev):
     with torch.cuda.graph(graph):
         rc = fast.prefill(*g.args(), out, ns, 0)
     assert rc == 1
+
+
+@pytest.mark.parametrize("lens,hqk,hv,gates", [(None, 16, 32, "strong"), ([700, 5, 64, 129], 4, 8, "mild")])
+def test_prefill_fused_kernel_variant(dev, lens, hqk, hv, gates):
+    """The fused kernel (prep waves building each chunk's T', P' and gates in LDS beside the
+    scan waves; variant 3) matches the oracle and the default path bit for bit."""
+    from gdn_hip.api import set_prefill_variant
+
+    lens = lens or varlen_lengths(16, seed=5)
+    inp = prefill_inputs(lens, hqk=hqk, hv=hv, seed=55, with_state=True, gates=gates)
+    ref_o, ref_s = _oracle(inp)
+    g = inp.to(dev)
+    try:
+        set_prefill_variant(3)
+        o3, s3 = gdn_prefill(*g.args())
+        set_prefill_variant(2)
+        o2, s2 = gdn_prefill(*g.args())
+    finally:
+        set_prefill_variant(0)
+    torch.cuda.synchronize()
+    _check(o3, s3, ref_o, ref_s, f"fused hqk={hqk} hv={hv} {gates}")
+    assert torch.equal(o3, o2) and torch.equal(s3, s2)
