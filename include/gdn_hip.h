@@ -104,7 +104,10 @@ typedef struct gdn_prefill_params {
     int32_t head_size;    /* D (must be 128) */
     float scale;
     int32_t cu_seqlens_int64; /* 1: int64 cu_seqlens, 0: int32 */
-    int32_t variant;      /* kernel variant for tuning sweeps; 0 = tuned default */
+    int32_t variant;      /* 0 = tuned default. Tuning variants, all scanning whole
+                             sequences (no segments): 1 / 2 force 4 / 8 scan waves
+                             per workgroup; 3 = fused prep + scan kernel
+                             (bit-identical to 2, slower on MI355X) */
     int32_t reserved;     /* 0 */
     const void *q;        int64_t q_stride[3];
     const void *k;        int64_t k_stride[3];
