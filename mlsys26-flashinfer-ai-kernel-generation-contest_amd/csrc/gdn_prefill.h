@@ -12,10 +12,11 @@
 // Networks"). Only non-positive log differences are exponentiated, so strong
 // decay underflows to 0 instead of overflowing; no clamping.
 //
-// Three launches on the caller's stream:
-//   plan  (1 + Z workgroups): sequence -> chunk tables from cu_seqlens on the
-//         device (no host sync), longest-first sequence order, and zero-fill of
-//         output rows that belong to no sequence.
+// Launches on the caller's stream:
+//   plan  (1 + Z workgroups): sequence -> chunk tables from cu_seqlens on the device
+//         (no host sync), longest-first sequence order, and zero-fill of output rows
+//         that belong to no sequence. Skipped for 1 to 64 sequences, where the prep
+//         kernel does the same work itself (PrepArgs::self_plan).
 //   prep  (chunks x q/k heads): K K^T and Q K^T on MFMA, gates, cumulative log
 //         decay, T = (I + A)^-1 (16x16 diagonal blocks by fp32 substitution,
 //         off-diagonal blocks on split-bf16 MFMA), P; writes per (chunk, v-head) records.
@@ -209,7 +210,10 @@ constexpr float kSegChainChunks = 0.9f;
 struct PlanArgs {
     const void *cu;
     int cu64, N, T, HO, nc;  // nc: chunk-table capacity (workspace bound)
-    int32_t *header, *chunk_tok0, *chunk_len, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
+    int32_t *header, *chunk_tok0, *chunk_len, *seq_chunk0, *seq_tok0, *seq_len;
+    // longest-first order: seq_rank[4 r .. 4 r + 3] = {sequence, first token, length, first
+    // chunk} of the r-th longest sequence (one 16-byte load per scan workgroup)
+    int32_t *seq_rank;
     bf16_t *out;
     int64_t o_st, o_sh;
     // segments (seg_G >= 3): at most seg_G segments per sequence; job entries of 8 ints
@@ -220,6 +224,73 @@ struct PlanArgs {
 };
 
 constexpr int kPlanSortMax = 512;
+
+// Segment job tables, built by one thread from the longest-first order and each
+// sequence's first chunk (clamped to nc) and token count.
+__device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const int32_t *first,
+                                 const int32_t *len)
+{
+    auto put = [&](int idx, int n, int kind, int cb, int ce, int q, int steps, int last) {
+        int32_t *e = p.jobs + 8 * idx;
+        e[0] = n;
+        e[1] = kind;
+        e[2] = cb;
+        e[3] = ce;
+        e[4] = q;
+        e[5] = steps;
+        e[6] = last;
+    };
+    // pass A: every segment 0 first (longest sequences first), then the state maps; slots
+    // q .. q + G - 2 of a sequence hold S_in(1) and M_s, R_s of the middle segments s
+    // (slot q + s - 1)
+    int na = 0, nc3 = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        int qs = 0;
+        for (int i = 0; i < p.N; ++i) {
+            const int n = order[i];
+            const int f = first[n], e = min(f + (len[n] + kC - 1) / kC, p.nc);
+            const int ncks = e - f;
+            int G = min(p.seg_G, max(1, ncks / kSegMinChunks));
+            const int Ls = (ncks + G - 1) / G;
+            G = Ls > 0 ? (ncks + Ls - 1) / Ls : 1;
+            if (G < 3)
+                G = 1;  // two segments would run one after the other
+            // boundary of segment sg: balanced lengths (see kSegFirstWeight) when every
+            // segment keeps at least 2 chunks, else equal lengths
+            const float base = (ncks + kSegChainChunks * (G - 1) * (G - 2) / 2) /
+                               (kSegFirstWeight + G - 1);
+            const bool bal = G > 1 && base - kSegChainChunks * (G - 2) >= 2.f &&
+                             kSegFirstWeight * base >= 2.f;
+            auto bnd = [&](int sg) {
+                if (sg >= G)
+                    return ncks;
+                if (!bal)
+                    return min(sg * Ls, ncks);
+                // chunks before segment sg: kSegFirstWeight base + sum over u = 1 .. sg - 1
+                // of (base - kSegChainChunks (u - 1))
+                const float x = kSegFirstWeight * base + (sg - 1) * base -
+                                kSegChainChunks * (sg - 1) * (sg - 2) / 2;
+                return min(max((int)(x + 0.5f), sg), ncks);
+            };
+            const int q = G > 1 ? qs : -1;
+            qs += G - 1;
+            if (pass == 0) {
+                put(na++, n, kJobFirst, 0, G > 1 ? bnd(1) : ncks, q, 0, 0);
+                continue;
+            }
+            for (int sg = 1; sg < G; ++sg) {
+                const int cb = bnd(sg), ce = bnd(sg + 1);
+                if (sg < G - 1) {
+                    put(na++, n, kJobZero, cb, ce, q + sg - 1, 0, 0);
+                    put(na++, n, kJobIdent, cb, ce, q + sg - 1, 0, 0);
+                }
+                put(p.seg_capA + nc3++, n, kJobResume, cb, ce, q, sg - 1, sg == G - 1);
+            }
+        }
+    }
+    p.header[1] = na;
+    p.header[2] = nc3;
+}
 
 // ------------------------------------------------------------------------- LDS copies
 #define GDN_LDS __attribute__((address_space(3)))
@@ -257,7 +328,15 @@ struct PrepArgs {
     char *records;
     int HQK, HV, ratio;
     float scale;
+    // Self-planned launch (1 <= N <= kSelfPlanMax; no plan kernel): every workgroup finds
+    // its units' chunks from cu_seqlens itself, the last block writes the tables the scan reads
+    // (plan.header, seq_*, jobs) and the workgroups zero-fill the output rows outside every
+    // sequence. Otherwise the plan kernel ran first and header / chunk_* hold its tables.
+    int self_plan;
+    PlanArgs plan;
 };
+
+constexpr int kSelfPlanMax = 64;  // one sequence per lane of a wave
 
 // ------------------------------------------------------------------------- scan
 struct ScanArgs {
@@ -267,7 +346,7 @@ struct ScanArgs {
     bf16_t *out;
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;
     int64_t st_sn, st_sh, st_sv, ns_sn, ns_sh, ns_sv;
-    const int32_t *header, *seq_chunk0, *seq_order, *seq_tok0, *seq_len;
+    const int32_t *header, *seq_chunk0, *seq_tok0, *seq_len, *seq_rank;
     const char *records;
     int HQK, HV, ratio, ngroups;
     // Segment jobs (jobs != nullptr): the grid walks entries jobs[8 (job_first + e)] =

@@ -29,7 +29,7 @@ int seg_count(int64_t T, int64_t N, int64_t HV)
 
 struct Layout {
     int64_t nc;
-    int64_t header, chunk_tok0, chunk_len, seq_chunk0, seq_order, seq_tok0, seq_len, records,
+    int64_t header, chunk_tok0, chunk_len, seq_chunk0, seq_rank, seq_tok0, seq_len, records,
         total;
     int G;                // segments per sequence at most (1: none)
     int64_t capA, capC;   // pass A / pass C job capacity
@@ -52,8 +52,8 @@ Layout layout(int64_t T, int64_t N, int64_t HV)
     o += L.nc * 4;
     L.seq_chunk0 = o;
     o += (N + 1) * 4;
-    L.seq_order = o;
-    o += N * 4;
+    L.seq_rank = (o + 15) & ~int64_t(15);
+    o = L.seq_rank + N * 16;
     L.seq_tok0 = o;
     o += N * 4;
     L.seq_len = o;
@@ -192,7 +192,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     pa.chunk_tok0 = (int32_t *)(ws + L.chunk_tok0);
     pa.chunk_len = (int32_t *)(ws + L.chunk_len);
     pa.seq_chunk0 = (int32_t *)(ws + L.seq_chunk0);
-    pa.seq_order = (int32_t *)(ws + L.seq_order);
+    pa.seq_rank = (int32_t *)(ws + L.seq_rank);
     pa.seq_tok0 = (int32_t *)(ws + L.seq_tok0);
     pa.seq_len = (int32_t *)(ws + L.seq_len);
     pa.out = (gdn::bf16_t *)p->output;
@@ -211,14 +211,21 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     pa.seg_G = G;
     pa.seg_capA = (int)L.capA;
     pa.jobs = G > 1 ? (int32_t *)(ws + L.jobs) : nullptr;
+    // Up to 64 sequences the prep kernel plans for itself (one dependent launch fewer:
+    // the plan kernel's ~5 us sat on the critical path, mostly cu_seqlens load latency).
+    const bool prep_runs = L.nc > 0 && T > 0 && !fused;
+    const bool self_plan = prep_runs && N >= 1 && N <= gdn::kSelfPlanMax;
     gdn_begin_launches();
-    hipLaunchKernelGGL(gdn::gdn_prefill_plan_kernel, dim3(1 + kZeroFillBlocks), dim3(256), 0,
-                       st, pa);
-    int rc = gdn_check_launch("gdn_prefill_plan_kernel");
-    if (rc)
-        return rc;
+    int rc = 0;
+    if (!self_plan) {
+        hipLaunchKernelGGL(gdn::gdn_prefill_plan_kernel, dim3(1 + kZeroFillBlocks), dim3(256),
+                           0, st, pa);
+        rc = gdn_check_launch("gdn_prefill_plan_kernel");
+        if (rc)
+            return rc;
+    }
 
-    if (L.nc > 0 && T > 0 && !fused) {
+    if (prep_runs) {
         gdn::PrepArgs qa;
         qa.q = (const gdn::bf16_t *)p->q;
         qa.k = (const gdn::bf16_t *)p->k;
@@ -244,6 +251,8 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         qa.HV = HV;
         qa.ratio = ratio;
         qa.scale = p->scale;
+        qa.self_plan = self_plan ? 1 : 0;
+        qa.plan = pa;
         // persistent: two workgroups per CU walk the (chunk, q/k head, v-head pair) units
         const int vh = ratio % 2 == 0 ? 2 : 1;
         const int64_t units = L.nc * HQK * (ratio / vh);
@@ -285,7 +294,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         sa.ns_sv = p->new_state_stride[2];
         sa.header = pa.header;
         sa.seq_chunk0 = pa.seq_chunk0;
-        sa.seq_order = pa.seq_order;
+        sa.seq_rank = pa.seq_rank;
         sa.seq_tok0 = pa.seq_tok0;
         sa.seq_len = pa.seq_len;
         sa.records = ws + L.records;

@@ -57,6 +57,9 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                         p.chunk_tok0[first + i] = t0 + i * kC;
                         p.chunk_len[first + i] = min(kC, ln - i * kC);
                     }
+                    // too many sequences to sort: identity order
+                    *(int4 *)(p.seq_rank + 4 * n) =
+                        int4{n, t0, ln, (int32_t)(first < p.nc ? first : p.nc)};
                 }
             }
             __syncthreads();  // every lane has read s_carry and s_wtot
@@ -86,9 +89,9 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                 p.chunk_len[c] = min(kC, s_len[lo] - i * kC);
             }
         }
-        // Longest-first order (identity when N is large).
+        // Longest-first order (identity when N is large, written above).
         __shared__ int32_t s_order[kPlanSortMax];
-        if (p.N <= kPlanSortMax) {
+        if (par) {
             for (int n = tid; n < p.N; n += 256) {
                 const int mine = s_nck[n];
                 int rank = 0;
@@ -96,76 +99,14 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                     const int o = s_nck[m];
                     rank += (o > mine) || (o == mine && m < n);
                 }
-                p.seq_order[rank] = n;
+                *(int4 *)(p.seq_rank + 4 * rank) = int4{n, s_t0[n], s_len[n], s_first[n]};
                 s_order[rank] = n;
             }
-        } else {
-            for (int n = tid; n < p.N; n += 256)
-                p.seq_order[n] = n;
         }
         if (p.seg_G >= 3 && par) {  // segment job tables (host only asks for small N)
             __syncthreads();
-            if (tid == 0) {
-                auto put = [&](int idx, int n, int kind, int cb, int ce, int q, int steps, int last) {
-                    int32_t *e = p.jobs + 8 * idx;
-                    e[0] = n;
-                    e[1] = kind;
-                    e[2] = cb;
-                    e[3] = ce;
-                    e[4] = q;
-                    e[5] = steps;
-                    e[6] = last;
-                };
-                // pass A: every segment 0 first (longest sequences first), then the state
-                // maps; slots q .. q + G - 2 of a sequence hold S_in(1) and M_s, R_s of the
-                // middle segments s (slot q + s - 1)
-                int na = 0, nc3 = 0;
-                for (int pass = 0; pass < 2; ++pass) {
-                    int qs = 0;
-                    for (int i = 0; i < p.N; ++i) {
-                        const int n = s_order[i];
-                        const int ncks = s_end[n] - s_first[n];
-                        int G = min(p.seg_G, max(1, ncks / kSegMinChunks));
-                        const int Ls = (ncks + G - 1) / G;
-                        G = Ls > 0 ? (ncks + Ls - 1) / Ls : 1;
-                        if (G < 3)
-                            G = 1;  // two segments would run one after the other
-                        // boundary of segment sg: balanced lengths (see kSegFirstWeight) when
-                        // every segment keeps at least 2 chunks, else equal lengths
-                        const float base = (ncks + kSegChainChunks * (G - 1) * (G - 2) / 2) /
-                                           (kSegFirstWeight + G - 1);
-                        const bool bal = G > 1 && base - kSegChainChunks * (G - 2) >= 2.f &&
-                                         kSegFirstWeight * base >= 2.f;
-                        auto bnd = [&](int sg) {
-                            if (sg >= G)
-                                return ncks;
-                            if (!bal)
-                                return min(sg * Ls, ncks);
-                            // chunks before segment sg: kSegFirstWeight base + sum over
-                            // u = 1 .. sg - 1 of (base - kSegChainChunks (u - 1))
-                            const float x = kSegFirstWeight * base + (sg - 1) * base -
-                                            kSegChainChunks * (sg - 1) * (sg - 2) / 2;
-                            return min(max((int)(x + 0.5f), sg), ncks);
-                        };
-                        const int q = G > 1 ? qs : -1;
-                        qs += G - 1;
-                        if (pass == 0) {
-                            put(na++, n, kJobFirst, 0, G > 1 ? bnd(1) : ncks, q, 0, 0);
-                            continue;
-                        }
-                        for (int sg = 1; sg < G; ++sg) {
-                            const int cb = bnd(sg), ce = bnd(sg + 1);
-                            if (sg < G - 1) {
-                                put(na++, n, kJobZero, cb, ce, q + sg - 1, 0, 0);
-                                put(na++, n, kJobIdent, cb, ce, q + sg - 1, 0, 0);
-                            }
-                            put(p.seg_capA + nc3++, n, kJobResume, cb, ce, q, sg - 1, sg == G - 1);
-                        }
-                    }
-                }
-                p.header[1] = na;
-                p.header[2] = nc3;
-            }
+            if (tid == 0)
+                plan_jobs(p, s_order, s_first, s_len);
         }
         return;
     }

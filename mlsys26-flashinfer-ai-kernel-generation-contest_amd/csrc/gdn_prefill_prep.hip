@@ -30,18 +30,103 @@ struct PrepSmem {
     u32x4 XA[VH][4][64];  // X_w in A-operand layout, by lane, split4
     u32x4 AO[VH][6][64];  // off-diagonal A_im (m < i) as XA; index i(i-1)/2 + m
     float Ms[4 * VH][16][16];  // per wave: -A_ww rows, X_w, then T' staging
+    // self-planned launches: sequence n's first chunk (clamped to nc; nc past the N
+    // sequences), first token and length; the chunk total and the covered tokens [g0, g1)
+    int32_t s_first[kSelfPlanMax], s_t0[kSelfPlanMax], s_len[kSelfPlanMax];
+    int32_t s_total, s_g0, s_g1, s_pad;
 };
 
 constexpr int kGateWave = 3;  // column block with no work after the barrier
+
+// Self-planned launch: wave 0 of every workgroup builds the sequence table in LDS from
+// cu_seqlens, with the plan kernel's clamps (gdn_prefill_plan.hip), so both give the same
+// chunk numbering; the last block, which walks the fewest units, then writes what the scan
+// reads (sequence tables, longest-first order, chunk total, segment jobs) and every
+// workgroup zero-fills its share of the output rows outside [cu[0], cu[N]).
+template <int VH>
+__device__ __forceinline__ void self_plan(const PrepArgs &p, PrepSmem<VH> &sm, int wv, int l)
+{
+    const PlanArgs &q = p.plan;
+    if (wv == 0) {
+        int t0 = 0, ln = 0;
+        int64_t nck = 0, braw = 0;
+        if (l < q.N) {
+            int64_t a = load_cu(q.cu, q.cu64, l), b = load_cu(q.cu, q.cu64, l + 1);
+            braw = b;
+            a = a < 0 ? 0 : (a > q.T ? q.T : a);
+            b = b < a ? a : (b > q.T ? q.T : b);
+            t0 = (int)a;
+            ln = (int)(b - a);
+            nck = (ln + kC - 1) / kC;
+        }
+        const int64_t incl = wave_prefix_sum_i64(nck), first = incl - nck;
+        sm.s_first[l] = l < q.N ? (int32_t)(first < q.nc ? first : q.nc) : q.nc;
+        sm.s_t0[l] = t0;
+        sm.s_len[l] = ln;
+        if (l == 63)
+            sm.s_total = (int32_t)(incl < q.nc ? incl : q.nc);
+        // Cross-lane reads stay in wave-uniform control flow: inside a lane-conditional
+        // branch the compiler may reuse the source register in lanes outside the branch.
+        const int last = q.N - 1;
+        const int64_t b_hi = __builtin_amdgcn_readlane((int)(braw >> 32), last),
+                      b_lo = (uint32_t)__builtin_amdgcn_readlane((int)braw, last);
+        const int64_t g1 = (b_hi << 32) | b_lo;
+        const int g0 = __builtin_amdgcn_readlane(t0, 0);  // cu[0] clamped to [0, T]
+        if (l == 0) {
+            sm.s_g0 = g0;
+            sm.s_g1 = (int32_t)(g1 < g0 ? g0 : (g1 > q.T ? q.T : g1));
+        }
+    }
+    __syncthreads();
+    if (blockIdx.x == gridDim.x - 1 && wv == 0) {
+        const int first = sm.s_first[l], t0 = sm.s_t0[l], ln = sm.s_len[l];
+        const int nck = (ln + kC - 1) / kC;
+        int rank = 0;
+        for (int m = 0; m < q.N; ++m) {
+            const int o = __builtin_amdgcn_readlane(nck, m);
+            rank += (o > nck) || (o == nck && m < l);
+        }
+        // the second K buffer is not written before the first unit's barrier
+        int32_t *order = (int32_t *)sm.K[1];
+        if (l < q.N) {
+            q.seq_tok0[l] = t0;
+            q.seq_len[l] = ln;
+            q.seq_chunk0[l] = first;
+            *(int4 *)(q.seq_rank + 4 * rank) = int4{l, t0, ln, first};
+            order[rank] = l;
+        }
+        if (l == 0) {
+            q.seq_chunk0[q.N] = sm.s_total;
+            q.header[0] = sm.s_total;
+        }
+        if (q.seg_G >= 3 && l == 0)
+            plan_jobs(q, order, sm.s_first, sm.s_len);
+    }
+    const int g0 = sm.s_g0, g1 = sm.s_g1, gap = g0 + (q.T - g1);
+    if (gap > 0) {
+        const int per_tok = q.HO * (kDK / 8);
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        for (int gt = blockIdx.x; gt < gap; gt += gridDim.x) {
+            const int64_t tok = gt < g0 ? gt : g1 + (gt - g0);
+            for (int v = threadIdx.x; v < per_tok; v += blockDim.x)
+                *(u32x4 *)(q.out + tok * q.o_st + (v >> 4) * q.o_sh + (v & 15) * 8) = z;
+        }
+    }
+}
 
 template <int VH>
 __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 {
     const int ngrp = p.ratio / VH;
-    const int nunits = p.header[0] * p.HQK * ngrp;
     // wv is wave-uniform: branches on the column block are scalar branches
     const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
               lr = l & 15, lg = l >> 4;
+    if (p.self_plan)
+        self_plan(p, sm, wv, l);
+    // (values read from LDS are uniform here; readfirstlane tells the compiler so, or every
+    // branch on them would become a divergent one)
+    const int nunits =
+        (p.self_plan ? __builtin_amdgcn_readfirstlane(sm.s_total) : p.header[0]) * p.HQK * ngrp;
     // Waves are dealt to the 4 SIMDs round-robin: the second v-head takes the blocks in
     // reverse, so each SIMD pairs a heavy column block (w = 0) with a light one.
     const int hv = wv >> 2, w = hv & 1 ? 3 - (wv & 3) : (wv & 3);
@@ -56,8 +141,18 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         r.c = grp / p.HQK;
         r.g = grp % p.HQK;
         r.h = r.g * p.ratio + hg * VH + hv;
-        r.tok0 = p.chunk_tok0[r.c];
-        r.len = p.chunk_len[r.c];
+        if (p.self_plan) {
+            // the owner of chunk c is the last sequence whose first chunk is <= c (first
+            // chunks never decrease; an empty sequence shares its successor's first chunk)
+            const int f = sm.s_first[l];
+            const int n = __popcll(__ballot(f <= r.c)) - 1;
+            const int i = r.c - __builtin_amdgcn_readlane(f, n);
+            r.tok0 = __builtin_amdgcn_readfirstlane(sm.s_t0[n]) + kC * i;
+            r.len = min(kC, __builtin_amdgcn_readfirstlane(sm.s_len[n]) - kC * i);
+        } else {
+            r.tok0 = p.chunk_tok0[r.c];
+            r.len = p.chunk_len[r.c];
+        }
         return r;
     };
     // K or Q of a unit -> LDS: 16 windows of 64 16-byte units (4 rows each) per matrix,

@@ -43,7 +43,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     const int grp = (slot / gsz) * 8 + xcd;
     if (grp >= p.ngroups)
         return;
-    int n, kind = kJobFirst, cb = 0, ce = 0x7fffffff, q = -1, steps = 0, last = 0;
+    int n, tok0, len, c0, kind = kJobFirst, cb = 0, ce = 0x7fffffff, q = -1, steps = 0, last = 0;
     if constexpr (SEG) {
         const int e = grp / p.HQK;
         if (e >= p.header[p.njob_idx])
@@ -56,13 +56,19 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         q = je[4];
         steps = je[5];
         last = je[6];
+        tok0 = p.seq_tok0[n];
+        len = p.seq_len[n];
+        c0 = p.seq_chunk0[n];
     } else {
-        n = p.seq_order[grp / p.HQK];
+        const int4 r = *(const int4 *)(p.seq_rank + 4 * (grp / p.HQK));
+        n = r.x;
+        tok0 = r.y;
+        len = r.z;
+        c0 = r.w;
     }
     const int g = grp % p.HQK;
     const int h = g * p.ratio + wi / TPH;
     const int v0 = (wi % TPH) * 16 * NW;
-    const int tok0 = p.seq_tok0[n], len = p.seq_len[n], c0 = p.seq_chunk0[n];
     // records exist only for chunk ids < header[0] (see the plan kernel's clamp)
     const int nck = min((len + kC - 1) / kC, max(p.header[0] - c0, 0));
     ce = min(ce, nck);

@@ -208,16 +208,17 @@ def test_prefill_matches_exact_fixture(dev):
     _check(out, ns, f["out"], f["new_state"], "exact fixture")
 
 
-@pytest.mark.parametrize("nseq", [255, 300, 600])
+@pytest.mark.parametrize("nseq", [64, 65, 255, 300, 600])
 def test_prefill_many_sequences(dev, nseq):
-    """Hundreds of short and empty sequences: the planning kernel's chunk table and
-    longest-first order (its sort covers up to 512 sequences) drive prep and scan."""
+    """Many short and empty sequences. Up to 64 the prep kernel plans for itself (one
+    sequence per lane); from 65 the planning kernel's chunk table and longest-first order
+    (its sort covers up to 512 sequences) drive prep and scan."""
     g = torch.Generator().manual_seed(nseq)
     lens = [int(x) for x in torch.randint(0, 90, (nseq,), generator=g)]
     _run(dev, prefill_inputs(lens, hqk=4, hv=8, seed=nseq, with_state=True), f"N={nseq}")
 
 
-@pytest.mark.parametrize("nseq", [3, 300])
+@pytest.mark.parametrize("nseq", [3, 64, 300])
 def test_prefill_gap_before_first_sequence(dev, nseq):
     """cu_seqlens[0] > 0: the leading tokens belong to no sequence and read as zero."""
     g = torch.Generator().manual_seed(7 + nseq)
