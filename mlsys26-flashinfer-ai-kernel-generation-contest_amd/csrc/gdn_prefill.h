@@ -226,7 +226,12 @@ struct PlanArgs {
 constexpr int kPlanSortMax = 512;
 
 // Segment job tables, built by one thread from the longest-first order and each
-// sequence's first chunk (clamped to nc) and token count.
+// sequence's first chunk (clamped to nc) and token count. A sequence of at least
+// 3 kSegMinChunks chunks is cut into up to seg_G balanced segments; shorter ones stay whole
+// and run in whichever pass they lengthen least. When no cut pays off (sequences of similar
+// length, none much longer than the rest), every sequence runs whole in pass C and pass A
+// has no jobs. Estimates count in pass-C chunk times: a pass-A chunk with outputs weighs
+// 1 / kSegFirstWeight, a state-map chunk 1, a chain step kSegChainChunks.
 __device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const int32_t *first,
                                  const int32_t *len)
 {
@@ -240,51 +245,103 @@ __device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const 
         e[5] = steps;
         e[6] = last;
     };
-    // pass A: every segment 0 first (longest sequences first), then the state maps; slots
-    // q .. q + G - 2 of a sequence hold S_in(1) and M_s, R_s of the middle segments s
-    // (slot q + s - 1)
+    struct Cut {
+        int ncks, G, Ls;
+        float base;
+        bool bal;
+    };
+    auto cut = [&](int n) {
+        Cut c;
+        const int f = first[n], e = min(f + (len[n] + kC - 1) / kC, p.nc);
+        c.ncks = e - f;
+        int G = min(p.seg_G, max(1, c.ncks / kSegMinChunks));
+        c.Ls = (c.ncks + G - 1) / G;
+        G = c.Ls > 0 ? (c.ncks + c.Ls - 1) / c.Ls : 1;
+        if (G < 3)
+            G = 1;  // two segments would run one after the other
+        c.G = G;
+        // balanced lengths (see kSegFirstWeight) when every segment keeps at least 2
+        // chunks, else equal lengths
+        c.base = (c.ncks + kSegChainChunks * (G - 1) * (G - 2) / 2) / (kSegFirstWeight + G - 1);
+        c.bal = G > 1 && c.base - kSegChainChunks * (G - 2) >= 2.f &&
+                kSegFirstWeight * c.base >= 2.f;
+        return c;
+    };
+    // first chunk of segment sg
+    auto bnd = [&](const Cut &c, int sg) {
+        if (sg >= c.G)
+            return c.ncks;
+        if (!c.bal)
+            return min(sg * c.Ls, c.ncks);
+        // chunks before segment sg: kSegFirstWeight base + sum over u = 1 .. sg - 1 of
+        // (base - kSegChainChunks (u - 1))
+        const float x = kSegFirstWeight * c.base + (sg - 1) * c.base -
+                        kSegChainChunks * (sg - 1) * (sg - 2) / 2;
+        return min(max((int)(x + 0.5f), sg), c.ncks);
+    };
+    // pass spans of the cut sequences, then the whole ones greedily, longest first
+    float spanA = 0.f, spanC = 0.f;
+    int cmax = 0;
+    for (int i = 0; i < p.N; ++i) {
+        const Cut c = cut(order[i]);
+        cmax = max(cmax, c.ncks);
+        if (c.G == 1)
+            continue;
+        spanA = fmaxf(spanA, bnd(c, 1) / kSegFirstWeight);
+        for (int sg = 1; sg < c.G; ++sg) {
+            const int ls = bnd(c, sg + 1) - bnd(c, sg);
+            if (sg < c.G - 1)
+                spanA = fmaxf(spanA, (float)ls);
+            spanC = fmaxf(spanC, ls + kSegChainChunks * (sg - 1));
+        }
+    }
+    uint64_t in_c[2] = {0, 0};  // whole sequence n runs in pass C (n < 128: N HV 3 <= 256)
+    for (int i = 0; i < p.N; ++i) {
+        const int n = order[i];
+        const Cut c = cut(n);
+        if (c.G > 1)
+            continue;
+        const float a = c.ncks / kSegFirstWeight;
+        if (fmaxf(spanA, a) - spanA <= fmaxf(spanC, (float)c.ncks) - spanC) {
+            spanA = fmaxf(spanA, a);
+        } else {
+            spanC = fmaxf(spanC, (float)c.ncks);
+            in_c[n >> 6] |= uint64_t(1) << (n & 63);
+        }
+    }
+    // (a second pass with jobs adds about one chunk time of start-up)
+    const bool whole_all = cmax <= spanA + spanC + 1.f;
+    // pass A: every segment 0 and whole sequence first (longest sequences first), then the
+    // state maps; slots q .. q + G - 2 of a cut sequence hold S_in(1) and M_s, R_s of the
+    // middle segments s (slot q + s - 1)
     int na = 0, nc3 = 0;
     for (int pass = 0; pass < 2; ++pass) {
         int qs = 0;
         for (int i = 0; i < p.N; ++i) {
             const int n = order[i];
-            const int f = first[n], e = min(f + (len[n] + kC - 1) / kC, p.nc);
-            const int ncks = e - f;
-            int G = min(p.seg_G, max(1, ncks / kSegMinChunks));
-            const int Ls = (ncks + G - 1) / G;
-            G = Ls > 0 ? (ncks + Ls - 1) / Ls : 1;
-            if (G < 3)
-                G = 1;  // two segments would run one after the other
-            // boundary of segment sg: balanced lengths (see kSegFirstWeight) when every
-            // segment keeps at least 2 chunks, else equal lengths
-            const float base = (ncks + kSegChainChunks * (G - 1) * (G - 2) / 2) /
-                               (kSegFirstWeight + G - 1);
-            const bool bal = G > 1 && base - kSegChainChunks * (G - 2) >= 2.f &&
-                             kSegFirstWeight * base >= 2.f;
-            auto bnd = [&](int sg) {
-                if (sg >= G)
-                    return ncks;
-                if (!bal)
-                    return min(sg * Ls, ncks);
-                // chunks before segment sg: kSegFirstWeight base + sum over u = 1 .. sg - 1
-                // of (base - kSegChainChunks (u - 1))
-                const float x = kSegFirstWeight * base + (sg - 1) * base -
-                                kSegChainChunks * (sg - 1) * (sg - 2) / 2;
-                return min(max((int)(x + 0.5f), sg), ncks);
-            };
-            const int q = G > 1 ? qs : -1;
-            qs += G - 1;
-            if (pass == 0) {
-                put(na++, n, kJobFirst, 0, G > 1 ? bnd(1) : ncks, q, 0, 0);
+            const Cut c = cut(n);
+            const bool whole = whole_all || c.G == 1;
+            const bool wc = whole_all || (in_c[n >> 6] >> (n & 63) & 1);
+            if (whole) {
+                if (pass == 0 && !wc)
+                    put(na++, n, kJobFirst, 0, c.ncks, -1, 0, 0);
+                else if (pass == 1 && wc)
+                    put(p.seg_capA + nc3++, n, kJobFirst, 0, c.ncks, -1, 0, 0);
                 continue;
             }
-            for (int sg = 1; sg < G; ++sg) {
-                const int cb = bnd(sg), ce = bnd(sg + 1);
-                if (sg < G - 1) {
+            const int q = qs;
+            qs += c.G - 1;
+            if (pass == 0) {
+                put(na++, n, kJobFirst, 0, bnd(c, 1), q, 0, 0);
+                continue;
+            }
+            for (int sg = 1; sg < c.G; ++sg) {
+                const int cb = bnd(c, sg), ce = bnd(c, sg + 1);
+                if (sg < c.G - 1) {
                     put(na++, n, kJobZero, cb, ce, q + sg - 1, 0, 0);
                     put(na++, n, kJobIdent, cb, ce, q + sg - 1, 0, 0);
                 }
-                put(p.seg_capA + nc3++, n, kJobResume, cb, ce, q, sg - 1, sg == G - 1);
+                put(p.seg_capA + nc3++, n, kJobResume, cb, ce, q, sg - 1, sg == c.G - 1);
             }
         }
     }

@@ -4,6 +4,8 @@ Bars (gdn_hip.parity): output bf16 atol = rtol = 1e-2 (both-condition rule of
 FAQ.md:104-110); new_state fp32 elementwise rtol = 1e-3 / atol = 1e-4 and normwise
 relative error <= 1e-3.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -244,6 +246,35 @@ def test_prefill_segments_mixed(dev, lens, hqk, hv):
     segments per sequence, empty sequences."""
     _run(dev, prefill_inputs(lens, hqk=hqk, hv=hv, seed=43, with_state=True, gates="mild",
                              state_std=0.05), f"segments lens={lens}")
+
+
+@pytest.mark.parametrize("lens,plan", [
+    (varlen_lengths(8, seed=7), (0, 8)),  # 12, 11, 11, 8, 8, 7, 5, 2 chunks: no cut pays off
+    ([4096, 700, 650], (9, 7)),           # 64 chunks in 6 segments; 11-chunk ones whole in C
+])
+def test_prefill_segment_planner(dev, lens, plan):
+    """Segment plans on few sequences (qk4_v8 heads; mild decay, so every chained state
+    carries into the next segment). Sequences of similar length all run whole in pass C
+    with pass A empty; a long sequence is cut into segments while the short ones run whole
+    in pass C beside its resumed segments. The job counts the planner wrote (workspace
+    header: pass A, pass C) name the plan taken."""
+    from gdn_hip import _lib
+    from gdn_hip.api import _prefill_marshal
+    inp = prefill_inputs(lens, hqk=4, hv=8, seed=59, with_state=True, gates="mild",
+                         state_std=0.05)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out = torch.empty((g.q.shape[0], 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((len(lens), 8, 128, 128), dtype=torch.float32, device=dev)
+    P, _, _, copy_back, keep, stream = _prefill_marshal(*g.args(), out, ns)
+    assert not copy_back
+    rc = _lib.load().gdn_prefill_launch(ctypes.byref(P), ctypes.c_void_p(stream.cuda_stream))
+    assert rc == 0, _lib.load().gdn_last_error()
+    torch.cuda.synchronize()
+    header = keep[-1][:12].view(torch.int32).cpu().tolist()
+    print(f"[planner {lens[:3]}] pass A jobs {header[1]}, pass C jobs {header[2]}", flush=True)
+    assert (header[1], header[2]) == plan
+    _check(out, ns, ref_out, ref_ns, f"planner {plan}")
 
 
 def test_prefill_segments_inplace_state(dev):
