@@ -277,6 +277,21 @@ def test_prefill_segment_planner(dev, lens, plan):
     _check(out, ns, ref_out, ref_ns, f"planner {plan}")
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_prefill_segment_planner_random(dev, seed):
+    """Random mixes in the segment regime (2 to 10 sequences, qk4_v8 heads, N HV 3 <= 256):
+    long sequences that may be cut beside short and empty ones, so plans mix cut sequences,
+    whole jobs in either pass and the all-whole plan; mild decay keeps every chained state
+    significant."""
+    rng = np.random.default_rng(1000 + seed)
+    n = int(rng.integers(2, 11))
+    lens = [int(rng.choice([rng.integers(0, 3), rng.integers(1, 400), rng.integers(400, 1400),
+                             rng.integers(1400, 3200)], p=[0.1, 0.35, 0.35, 0.2]))
+            for _ in range(n)]
+    _run(dev, prefill_inputs(lens, hqk=4, hv=8, seed=70 + seed, with_state=True, gates="mild",
+                             state_std=0.05), f"planner mix {seed} lens={lens}")
+
+
 def test_prefill_segments_inplace_state(dev):
     """Segmented scan with new_state aliasing state: pass A reads the initial state only in
     segment 0's job, and only the last segment's pass-C job writes the final state."""
