@@ -292,6 +292,15 @@ def test_prefill_segment_planner_random(dev, seed):
                              state_std=0.05), f"planner mix {seed} lens={lens}")
 
 
+def test_prefill_segments_planned_by_the_plan_kernel(dev):
+    """Segments with more than 64 sequences (one v-head: N HV 3 <= 256 up to 85 sequences):
+    the plan kernel, not the prep kernel, builds the tables and the job lists."""
+    rng = np.random.default_rng(77)
+    lens = [int(x) for x in rng.integers(0, 40, 68)] + [2500, 1900]
+    _run(dev, prefill_inputs(lens, hqk=1, hv=1, seed=78, with_state=True, gates="mild",
+                             state_std=0.05), f"plan-kernel segments N={len(lens)}")
+
+
 def test_prefill_segments_inplace_state(dev):
     """Segmented scan with new_state aliasing state: pass A reads the initial state only in
     segment 0's job, and only the last segment's pass-C job writes the final state."""
