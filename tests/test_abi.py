@@ -172,3 +172,14 @@ def test_fast_path_extension_loads_and_declines_host_tensors():
     assert fast.decode(t(1, 1, 4, 128), t(1, 1, 4, 128), t(1, 1, 8, 128), f(1, 8, 128, 128),
                        f(8), t(1, 1, 8), f(8), t(1, 1, 8), 0.5, t(1, 1, 8, 128),
                        f(1, 8, 128, 128), 0) == 1
+
+
+def test_native_caller_loads_and_links():
+    """The native C++ caller (tests/native) resolves the library, the oracle and the HIP
+    runtime through its run paths; without a GPU it stops at the device check (77)."""
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "gdn_native_caller")
+    assert os.path.exists(exe), "run __graft_entry__.build()"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode in (0, 77), r.stdout + r.stderr
+    if r.returncode == 77:
+        assert "no HIP device" in r.stdout
