@@ -150,16 +150,17 @@ def _time_cpu(fn, budget_s, max_n=200):
             return el / n, n
 
 
-def cpu_baseline_decode(batch=64, budget_s=10.0):
+def cpu_baseline_decode(batch=64, budget_s=10.0, max_n=1000):
     """Time the float32 C oracle (a port of the reference arithmetic) on the host cores
-    over repeated full decode steps, up to ~budget_s seconds."""
+    over repeated full decode steps, up to ~budget_s seconds or max_n steps."""
     from gdn_hip.inputs import decode_bytes, decode_inputs
     from oracle import gdn_oracle as O
 
     cores, avail, total = _host_cores()
     inp = decode_inputs(batch, seed=0)
     args = (inp.q, inp.k, inp.v, inp.state, inp.A_log, inp.a, inp.dt_bias, inp.b, inp.scale)
-    sec, n = _time_cpu(lambda: O.decode(*args, precision="f32", threads=cores), budget_s)
+    sec, n = _time_cpu(lambda: O.decode(*args, precision="f32", threads=cores), budget_s,
+                       max_n=max_n)
     return dict(value=decode_bytes(batch) / sec / 1e9, unit="GB/s", cores=cores,
                 cores_available=avail, cores_host=total, kind="port",
                 us_per_step=sec * 1e6,
@@ -213,7 +214,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=6.0)
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU work for the decode B=64 baseline (B=1 takes "
+                         "0.15 of it, the prefill 0.6)")
     ap.add_argument("--only", choices=["all", "decode", "prefill", "prefill4k"], default="all",
                     help="run one path only (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -278,11 +281,11 @@ def main():
     if not args.no_cpu:
         log("cpu baselines (fp32 C oracle): decode B=64, decode B=1, prefill 16x varlen")
         cpu = cpu_baseline_decode(budget_s=args.cpu_budget)
-        cpu1 = cpu_baseline_decode(batch=1, budget_s=2.0)
+        cpu1 = cpu_baseline_decode(batch=1, budget_s=0.15 * args.cpu_budget, max_n=20000)
         cpu1.update(value=cpu1["us_per_step"], unit="us/step (lower is better)")
         cpu_more = {"decode_b1": cpu1}
         if not args.no_prefill:
-            cpu_more["prefill"] = cpu_baseline_prefill(budget_s=args.cpu_budget)
+            cpu_more["prefill"] = cpu_baseline_prefill(budget_s=0.6 * args.cpu_budget)
         log(f"cpu: {cpu['value']:.2f} GB/s on {cpu['cores']} of {cpu['cores_host']} cores")
     traffic = _traffic_from_profile("decode_b64_traffic.txt")
     rec = {
