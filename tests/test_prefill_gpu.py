@@ -65,7 +65,7 @@ def test_prefill_long_memory_gates(dev, gates):
                              state_std=0.1), f"gates={gates}")
 
 
-@pytest.mark.parametrize("hqk,hv", [(4, 8), (8, 8), (2, 8), (1, 4)])
+@pytest.mark.parametrize("hqk,hv", [(4, 8), (8, 8), (2, 8), (1, 4), (2, 6), (1, 3)])
 def test_prefill_head_layouts(dev, hqk, hv):
     _run(dev, prefill_inputs([150, 90, 257], hqk=hqk, hv=hv, seed=9, with_state=True),
          f"hqk={hqk} hv={hv}")
