@@ -199,6 +199,7 @@ constexpr int kJobResume = 3;  // from S_in(1) and (steps) chain steps; outputs;
 constexpr int64_t kSlotFloats = 128 * 128;
 constexpr int kMtUnits = 2048;
 constexpr int kSegMinChunks = 4;            // shortest segment (before balancing)
+constexpr int kSegMaxG = 16;                // segments per sequence at most
 // Segment lengths balance the two passes (measured on MI355X): a segment-0 chunk, which
 // writes outputs in pass A, costs ~1/0.83 of a state-map chunk, and each chain step
 // delays a pass-C segment by ~0.9 chunk-times, so segment s >= 1 gets 0.9 (s - 1) chunks
@@ -225,128 +226,153 @@ struct PlanArgs {
 
 constexpr int kPlanSortMax = 512;
 
-// Segment job tables, built by one thread from the longest-first order and each
-// sequence's first chunk (clamped to nc) and token count. A sequence of at least
-// 3 kSegMinChunks chunks is cut into up to seg_G balanced segments; shorter ones stay whole
-// and run in whichever pass they lengthen least. When no cut pays off (sequences of similar
-// length, none much longer than the rest), every sequence runs whole in pass C and pass A
-// has no jobs. Estimates count in pass-C chunk times: a pass-A chunk with outputs weighs
-// 1 / kSegFirstWeight, a state-map chunk 1, a chain step kSegChainChunks.
-__device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const int32_t *first,
-                                 const int32_t *len)
+// Maximum over the 64 lanes of non-negative values (the prefix pattern of
+// wave_prefix_sum_i64; lane 63 holds the total), returned to every lane.
+__device__ __forceinline__ float wave_max_nonneg(float x)
 {
-    auto put = [&](int idx, int n, int kind, int cb, int ce, int q, int steps, int last) {
+    x = fmaxf(x, dpp_or0<0x111, 0xF>(x));
+    x = fmaxf(x, dpp_or0<0x112, 0xF>(x));
+    x = fmaxf(x, dpp_or0<0x114, 0xF>(x));
+    x = fmaxf(x, dpp_or0<0x118, 0xF>(x));
+    x = fmaxf(x, dpp_or0<0x142, 0xA>(x));
+    x = fmaxf(x, dpp_or0<0x143, 0xC>(x));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+// Segment job tables, built by one wave with all 64 lanes active (at most 64 sequences:
+// the host asks for segments only then), lane i for the sequence of rank i (order[i],
+// longest first), from each sequence's first chunk (clamped to nc) and token count.
+//
+// Estimates count in pass-C chunk times: a pass-A chunk with outputs weighs
+// 1 / kSegFirstWeight, a state-map chunk 1, a chain step kSegChainChunks. A sequence of
+// at least 3 kSegMinChunks chunks is cut into G balanced segments (segment 0 weighted by
+// kSegFirstWeight, each later one kSegChainChunks chunks shorter than the one before, so
+// that both passes take `base` chunk times); G is the largest balanced count, at most
+// seg_G and len / kSegMinChunks, below the minimum of 2 base(G) over real G,
+// G* = 1 - w + sqrt(w^2 + w + len / h) with w = kSegFirstWeight, h = kSegChainChunks / 2.
+// Shorter sequences stay whole and run in whichever pass they lengthen least; a whole
+// job is a kJobFirst entry without a slot, which either pass runs. When the longest
+// sequence scanned whole is no longer than the two spans plus one chunk time (a second
+// pass's start), nothing is cut and every sequence runs whole in pass C.
+// Pass A lists every segment 0 and whole sequence first (rank order), then the state maps;
+// slots q .. q + G - 2 of a cut sequence hold S_in(1) and M_s, R_s of the middle segments
+// s (slot q + s - 1).
+__device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const int32_t *first,
+                                 const int32_t *len, int lane)
+{
+    constexpr float w = kSegFirstWeight, h = 0.5f * kSegChainChunks;
+    const bool act = lane < p.N;
+    const int n = act ? order[lane] : 0;
+    int ncks = 0;
+    if (act) {
+        const int f = first[n], e = min(f + (len[n] + kC - 1) / kC, p.nc);
+        ncks = e - f;
+    }
+    auto base_of = [&](int g) { return (ncks + h * (g - 1) * (g - 2)) / (w + g - 1); };
+    auto balanced = [&](int g, float b) {
+        return b - kSegChainChunks * (g - 2) >= 2.f && w * b >= 2.f;
+    };
+    int G = 1;
+    float base = 0.f;
+    const int gmax = min(p.seg_G, ncks / kSegMinChunks);
+    if (gmax >= 3) {
+        const float gs = 1.f - w + sqrtf(w * w + w + ncks / h);
+        int g = max(3, min(gmax, (int)gs));
+        float b = base_of(g);
+        while (g > 3 && !balanced(g, b))
+            b = base_of(--g);
+        G = g;
+        base = b;
+    }
+    const bool bal = G > 1 && balanced(G, base);
+    const int Ls = G > 1 ? (ncks + G - 1) / G : ncks;
+    if (G > 1 && !bal) {  // equal lengths: as many segments as Ls-chunk pieces
+        G = (ncks + Ls - 1) / Ls;
+        if (G < 3)
+            G = 1;
+    }
+    // first chunk of segment sg
+    auto bnd = [&](int sg) {
+        if (sg >= G)
+            return ncks;
+        if (!bal)
+            return min(sg * Ls, ncks);
+        const float x = w * base + (sg - 1) * base - h * (sg - 1) * (sg - 2);
+        return min(max((int)(x + 0.5f), sg), ncks);
+    };
+    // pass spans of the cut sequences
+    float sa = 0.f, sc = 0.f;
+    if (G > 1) {
+        sa = bnd(1) / w;
+        for (int sg = 1; sg < G; ++sg) {
+            const int ls = bnd(sg + 1) - bnd(sg);
+            if (sg < G - 1)
+                sa = fmaxf(sa, (float)ls);
+            sc = fmaxf(sc, ls + kSegChainChunks * (sg - 1));
+        }
+    }
+    float spanA = wave_max_nonneg(sa), spanC = wave_max_nonneg(sc);
+    const float cmax = wave_max_nonneg((float)ncks);
+    // whole sequences, longest first: each to the pass it lengthens least (ties: A); once
+    // one fits both spans, every shorter one does too
+    uint64_t in_c = 0;
+    for (int i = 0; i < p.N; ++i) {
+        const int gi = __builtin_amdgcn_readlane(G, i);
+        const float c = (float)__builtin_amdgcn_readlane(ncks, i);
+        if (gi > 1)
+            continue;
+        if (c / w <= spanA && c <= spanC)
+            break;
+        if (fmaxf(spanA, c / w) - spanA <= fmaxf(spanC, c) - spanC) {
+            spanA = fmaxf(spanA, c / w);
+        } else {
+            spanC = fmaxf(spanC, c);
+            in_c |= uint64_t(1) << i;
+        }
+    }
+    const bool whole_all = cmax <= spanA + spanC + 1.f;
+    const bool whole = whole_all || G == 1;
+    const bool wc = whole_all || ((in_c >> lane) & 1);
+    // job counts -> offsets (exclusive prefix sums in rank order)
+    const int firstA = act && !(whole && wc), mapsA = act && !whole ? 2 * (G - 2) : 0;
+    const int passC = !act ? 0 : whole ? (wc ? 1 : 0) : G - 1;
+    const int slots = act && !whole ? G - 1 : 0;
+    const int64_t iF = wave_prefix_sum_i64(firstA), iM = wave_prefix_sum_i64(mapsA),
+                  iC = wave_prefix_sum_i64(passC), iS = wave_prefix_sum_i64(slots);
+    const int totF = (int)__builtin_amdgcn_readlane((int)iF, 63),
+              totM = (int)__builtin_amdgcn_readlane((int)iM, 63),
+              totC = (int)__builtin_amdgcn_readlane((int)iC, 63);
+    int oF = (int)iF - firstA, oM = totF + (int)iM - mapsA, oC = p.seg_capA + (int)iC - passC;
+    const int q = (int)iS - slots;
+    auto put = [&](int idx, int kind, int cb, int ce, int slot, int steps, int last) {
         int32_t *e = p.jobs + 8 * idx;
         e[0] = n;
         e[1] = kind;
         e[2] = cb;
         e[3] = ce;
-        e[4] = q;
+        e[4] = slot;
         e[5] = steps;
         e[6] = last;
     };
-    struct Cut {
-        int ncks, G, Ls;
-        float base;
-        bool bal;
-    };
-    auto cut = [&](int n) {
-        Cut c;
-        const int f = first[n], e = min(f + (len[n] + kC - 1) / kC, p.nc);
-        c.ncks = e - f;
-        int G = min(p.seg_G, max(1, c.ncks / kSegMinChunks));
-        c.Ls = (c.ncks + G - 1) / G;
-        G = c.Ls > 0 ? (c.ncks + c.Ls - 1) / c.Ls : 1;
-        if (G < 3)
-            G = 1;  // two segments would run one after the other
-        c.G = G;
-        // balanced lengths (see kSegFirstWeight) when every segment keeps at least 2
-        // chunks, else equal lengths
-        c.base = (c.ncks + kSegChainChunks * (G - 1) * (G - 2) / 2) / (kSegFirstWeight + G - 1);
-        c.bal = G > 1 && c.base - kSegChainChunks * (G - 2) >= 2.f &&
-                kSegFirstWeight * c.base >= 2.f;
-        return c;
-    };
-    // first chunk of segment sg
-    auto bnd = [&](const Cut &c, int sg) {
-        if (sg >= c.G)
-            return c.ncks;
-        if (!c.bal)
-            return min(sg * c.Ls, c.ncks);
-        // chunks before segment sg: kSegFirstWeight base + sum over u = 1 .. sg - 1 of
-        // (base - kSegChainChunks (u - 1))
-        const float x = kSegFirstWeight * c.base + (sg - 1) * c.base -
-                        kSegChainChunks * (sg - 1) * (sg - 2) / 2;
-        return min(max((int)(x + 0.5f), sg), c.ncks);
-    };
-    // pass spans of the cut sequences, then the whole ones greedily, longest first
-    float spanA = 0.f, spanC = 0.f;
-    int cmax = 0;
-    for (int i = 0; i < p.N; ++i) {
-        const Cut c = cut(order[i]);
-        cmax = max(cmax, c.ncks);
-        if (c.G == 1)
-            continue;
-        spanA = fmaxf(spanA, bnd(c, 1) / kSegFirstWeight);
-        for (int sg = 1; sg < c.G; ++sg) {
-            const int ls = bnd(c, sg + 1) - bnd(c, sg);
-            if (sg < c.G - 1)
-                spanA = fmaxf(spanA, (float)ls);
-            spanC = fmaxf(spanC, ls + kSegChainChunks * (sg - 1));
-        }
-    }
-    uint64_t in_c[2] = {0, 0};  // whole sequence n runs in pass C (n < 128: N HV 3 <= 256)
-    for (int i = 0; i < p.N; ++i) {
-        const int n = order[i];
-        const Cut c = cut(n);
-        if (c.G > 1)
-            continue;
-        const float a = c.ncks / kSegFirstWeight;
-        if (fmaxf(spanA, a) - spanA <= fmaxf(spanC, (float)c.ncks) - spanC) {
-            spanA = fmaxf(spanA, a);
+    if (act) {
+        if (whole) {
+            put(wc ? oC : oF, kJobFirst, 0, ncks, -1, 0, 0);
         } else {
-            spanC = fmaxf(spanC, (float)c.ncks);
-            in_c[n >> 6] |= uint64_t(1) << (n & 63);
-        }
-    }
-    // (a second pass with jobs adds about one chunk time of start-up)
-    const bool whole_all = cmax <= spanA + spanC + 1.f;
-    // pass A: every segment 0 and whole sequence first (longest sequences first), then the
-    // state maps; slots q .. q + G - 2 of a cut sequence hold S_in(1) and M_s, R_s of the
-    // middle segments s (slot q + s - 1)
-    int na = 0, nc3 = 0;
-    for (int pass = 0; pass < 2; ++pass) {
-        int qs = 0;
-        for (int i = 0; i < p.N; ++i) {
-            const int n = order[i];
-            const Cut c = cut(n);
-            const bool whole = whole_all || c.G == 1;
-            const bool wc = whole_all || (in_c[n >> 6] >> (n & 63) & 1);
-            if (whole) {
-                if (pass == 0 && !wc)
-                    put(na++, n, kJobFirst, 0, c.ncks, -1, 0, 0);
-                else if (pass == 1 && wc)
-                    put(p.seg_capA + nc3++, n, kJobFirst, 0, c.ncks, -1, 0, 0);
-                continue;
-            }
-            const int q = qs;
-            qs += c.G - 1;
-            if (pass == 0) {
-                put(na++, n, kJobFirst, 0, bnd(c, 1), q, 0, 0);
-                continue;
-            }
-            for (int sg = 1; sg < c.G; ++sg) {
-                const int cb = bnd(c, sg), ce = bnd(c, sg + 1);
-                if (sg < c.G - 1) {
-                    put(na++, n, kJobZero, cb, ce, q + sg - 1, 0, 0);
-                    put(na++, n, kJobIdent, cb, ce, q + sg - 1, 0, 0);
+            put(oF, kJobFirst, 0, bnd(1), q, 0, 0);
+            for (int sg = 1; sg < G; ++sg) {
+                const int cb = bnd(sg), ce = bnd(sg + 1);
+                if (sg < G - 1) {
+                    put(oM++, kJobZero, cb, ce, q + sg - 1, 0, 0);
+                    put(oM++, kJobIdent, cb, ce, q + sg - 1, 0, 0);
                 }
-                put(p.seg_capA + nc3++, n, kJobResume, cb, ce, q, sg - 1, sg == c.G - 1);
+                put(oC++, kJobResume, cb, ce, q, sg - 1, sg == G - 1);
             }
         }
     }
-    p.header[1] = na;
-    p.header[2] = nc3;
+    if (lane == 0) {
+        p.header[1] = totF + totM;
+        p.header[2] = totC;
+    }
 }
 
 // ------------------------------------------------------------------------- LDS copies

@@ -15,14 +15,16 @@ int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 int64_t max_chunks(int64_t T, int64_t N) { return (T + kChunkH - 1) / kChunkH + N; }
 
 // Segments per sequence (the default variant only): when (sequence, v-head) pairs are too
-// few to fill 256 CUs, the largest G <= 8 whose pass-A jobs N HV (2 G - 3) still fit one
-// workgroup per CU; 1 means no segments (G = 2 would scan its halves one after the other).
+// few to fill 256 CUs, the largest G <= gdn::kSegMaxG whose pass-A jobs N HV (2 G - 3)
+// still fit one workgroup per CU; 1 means no segments (G = 2 would scan its halves one
+// after the other). The planner picks each sequence's count up to G from its length.
 int seg_count(int64_t T, int64_t N, int64_t HV)
 {
-    if (T <= 0 || N <= 0 || N * HV * 3 > 256)
+    // (the job planner runs one sequence per lane in the self-planned prep kernel)
+    if (T <= 0 || N <= 0 || N > gdn::kSelfPlanMax || N * HV * 3 > 256)
         return 1;
     int G = 3;
-    while (G < 8 && N * HV * (2 * (G + 1) - 3) <= 256)
+    while (G < gdn::kSegMaxG && N * HV * (2 * (G + 1) - 3) <= 256)
         ++G;
     return G;
 }

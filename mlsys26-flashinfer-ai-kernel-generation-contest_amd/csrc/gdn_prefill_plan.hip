@@ -1,5 +1,5 @@
-// Prefill plan kernel: sequence -> chunk tables from cu_seqlens on the device, longest-
-// first sequence order, segment job tables, zero-fill of rows outside every sequence.
+// Prefill plan kernel (more than 64 sequences): sequence -> chunk tables from cu_seqlens on
+// the device, longest-first sequence order, zero-fill of rows outside every sequence.
 #include "gdn_prefill.h"
 
 namespace gdn {
@@ -90,7 +90,6 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
             }
         }
         // Longest-first order (identity when N is large, written above).
-        __shared__ int32_t s_order[kPlanSortMax];
         if (par) {
             for (int n = tid; n < p.N; n += 256) {
                 const int mine = s_nck[n];
@@ -100,14 +99,10 @@ __global__ __launch_bounds__(256) void gdn_prefill_plan_kernel(PlanArgs p)
                     rank += (o > mine) || (o == mine && m < n);
                 }
                 *(int4 *)(p.seq_rank + 4 * rank) = int4{n, s_t0[n], s_len[n], s_first[n]};
-                s_order[rank] = n;
             }
         }
-        if (p.seg_G >= 3 && par) {  // segment job tables (host only asks for small N)
-            __syncthreads();
-            if (tid == 0)
-                plan_jobs(p, s_order, s_first, s_len);
-        }
+        // (segment job tables come from the prep kernel: segments are used up to 64
+        // sequences only, where the prep kernel plans for itself)
         return;
     }
     // Zero-fill output rows of tokens outside [cu[0], cu[N]).

@@ -292,9 +292,10 @@ def test_prefill_segment_planner_random(dev, seed):
                              state_std=0.05), f"planner mix {seed} lens={lens}")
 
 
-def test_prefill_segments_planned_by_the_plan_kernel(dev):
-    """Segments with more than 64 sequences (one v-head: N HV 3 <= 256 up to 85 sequences):
-    the plan kernel, not the prep kernel, builds the tables and the job lists."""
+def test_prefill_long_sequences_among_many_plan_kernel(dev):
+    """Two long sequences among 68 short ones with one v-head: more than 64 sequences, so
+    the plan kernel builds the tables and every sequence is scanned whole (the job planner,
+    and with it segments, serves up to 64 sequences)."""
     rng = np.random.default_rng(77)
     lens = [int(x) for x in rng.integers(0, 40, 68)] + [2500, 1900]
     _run(dev, prefill_inputs(lens, hqk=1, hv=1, seed=78, with_state=True, gates="mild",
