@@ -20,9 +20,17 @@ namespace gdn {
 // wave (hv, 3), which has the least work after the barrier, also computes the next unit's
 // gates and cumulative log2 decay L.
 // (gdn_prefill/solution/triton/kernel.py:60-79 form the same A, T and P.)
+// K and Q rows in LDS: row t, k-chunk c (k = 8c .. 8c + 7) at unit 16 t + (c ^ pswz(t & 15)).
+// The MFMA operand reads take rows in token order (P' blocks) and in the pi order of the
+// A blocks; with the plain XOR (c ^ t) the pi-ordered reads were 2-way bank conflicts, as
+// both 16-lane groups of a read cycle hit the same eight units. Flipping bit 1 with bit 0
+// of the row makes both orders conflict-free under the b128 bank model (one cycle: a
+// 32-lane half with equal parity of lane bits 2, 3, 4; 16 distinct units mod 256 bytes).
+__device__ __forceinline__ int pswz(int r) { return r ^ ((r & 1) << 1); }
+
 template <int VH>
 struct PrepSmem {
-    u32x4 K[2][kC * 16];  // row t, k-chunk c at unit 16 t + (c ^ (t & 15))
+    u32x4 K[2][kC * 16];  // row t, k-chunk c at unit 16 t + (c ^ pswz(t & 15))
     u32x4 Q[kC * 16];
     float L[2][VH][64];    // L by token: L = L_hi + L_lo (float-float), L_hi here
     float Llo[2][VH][64];  // L_lo by token
@@ -166,7 +174,8 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         for (int i = 0; i < 4 / VH; ++i) {
             const int b = wv + 4 * VH * i;
             const int t = 4 * b + (l >> 4), cs = l & 15;
-            dma16(base + (uint32_t)min(t, U.len - 1) * st2 + 16u * (cs ^ (t & 15)), &dst[64 * b]);
+            dma16(base + (uint32_t)min(t, U.len - 1) * st2 + 16u * (cs ^ pswz(t & 15)),
+                  &dst[64 * b]);
         }
     };
     // Gates (gdn_decode/solution/triton/kernel.py:128-131); padding tokens: alpha = 1,
@@ -224,7 +233,7 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
 
     // MFMA operand: 16 rows, k-chunk 4 ks + lg.
     auto kop = [&](const u32x4 *M, int row, int ks) {
-        return M[16 * row + ((4 * ks + lg) ^ (row & 15))];
+        return M[16 * row + ((4 * ks + lg) ^ pswz(row & 15))];
     };
     float (*Ms)[16] = sm.Ms[wv];
 
