@@ -235,7 +235,15 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
     auto kop = [&](const u32x4 *M, int row, int ks) {
         return M[16 * row + ((4 * ks + lg) ^ pswz(row & 15))];
     };
+    // Per-wave 16 x 16 fp32 tile: element (r, c) at column c ^ 4 (r / 4). Rows in pi order
+    // (substitution, X_w) and in token order (transposes, T' staging) then read and write
+    // without bank conflicts; 4-column groups stay contiguous for the f32x4 row reads.
+    // (rows pi(lr) have r / 4 = lr % 4)
     float (*Ms)[16] = sm.Ms[wv];
+    auto ms = [&](int r, int c, int rq) -> float & { return Ms[r][c ^ (rq << 2)]; };
+    auto ms_row4 = [&](int r, int q, int rq) -> const f32x4 & {
+        return *(const f32x4 *)&Ms[r][4 * (q ^ rq)];
+    };
 
     // Diagonal-block masks of this lane, one bit per element: bits 0..3 keep P'[t][j] for
     // j <= t (t = 16 w + lr, j = 16 w + 4 lg + e), bits 4..7 keep A[t][j] for j < t
@@ -344,12 +352,12 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         f32x4 xw;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            Ms[pi16(lr)][4 * e + lg] = -Aww[e];
+            ms(pi16(lr), 4 * e + lg, lr & 3) = -Aww[e];
         {
             float arow[16];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const f32x4 v = *(const f32x4 *)&Ms[pi16(lr)][4 * q];
+                const f32x4 v = ms_row4(pi16(lr), q, lr & 3);
                 arow[4 * q] = v[0]; arow[4 * q + 1] = v[1]; arow[4 * q + 2] = v[2]; arow[4 * q + 3] = v[3];
             }
             float x[4];
@@ -374,11 +382,11 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
         // X_w in B-operand layout (lane (n, lg) element s = X[4 s + lg][n]) via the scratch
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
-            Ms[pi16(lr)][lg + 4 * s2] = xw[s2];
+            ms(pi16(lr), lg + 4 * s2, lr & 3) = xw[s2];
         f32x4 TB[4];
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
-            TB[0][s2] = Ms[4 * s2 + lg][lr];
+            TB[0][s2] = ms(4 * s2 + lg, lr, s2);
         // every X_i is in XA, every A_im in AO; every wave is done with Q (the next unit's K
         // copy stays in flight)
         lds_barrier_inflight();
@@ -435,8 +443,8 @@ __device__ __forceinline__ void prep_body(const PrepArgs &p, PrepSmem<VH> &sm)
                 break;
 #pragma unroll
             for (int s2 = 0; s2 < 4; ++s2)
-                Ms[4 * s2 + lg][lr] = TB[i][s2] * bcol;
-            const f32x4 v = *(const f32x4 *)&Ms[l >> 2][4 * (l & 3)];
+                ms(4 * s2 + lg, lr, s2) = TB[i][s2] * bcol;
+            const f32x4 v = ms_row4(l >> 2, l & 3, lg);
             uint32_t h01, l01, h23, l23;
             split_bf16x2(v[0], v[1], h01, l01);
             split_bf16x2(v[2], v[3], h23, l23);
