@@ -566,6 +566,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         // never wait on the MFMA chain that produced them.
         f32x4 Oi[2], Oa[2];
         float sg[2];
+        // one store per output tile: the chunk barrier leaves exactly these four in flight
         auto out_epi = [&](int tt) {
             const int cb = tt & 1;
             const uint32_t o01 = pack_bf16x2(fmaf(sg[cb], Oi[cb][0], Oa[cb][0]), fmaf(sg[cb], Oi[cb][1], Oa[cb][1]));
@@ -621,12 +622,29 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         phase1(B, Bn, ncs, more);
         phase2(B, c);
     };
+    // The barrier before a chunk waits for this wave's copies of it (vector memory
+    // operations complete in issue order). After the first chunk, a job with outputs
+    // has issued exactly four more operations since those copies: the previous chunk's
+    // output stores, which nothing in the kernel reads, so it leaves them in flight
+    // (waiting for them cost ~700 of a chunk's ~7000 cycles). Before the first chunk,
+    // state loads the compiler may have ordered either way are in flight: wait for all.
+    const bool keep_stores = !FUSED && do_out;
+    auto chunk_barrier = [&](bool first) {
+        if (keep_stores && !first) {
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        } else {
+            dma_barrier();
+        }
+    };
     for (int c = cb; c < ce; c += 2) {
-        dma_barrier();  // chunk c is in BA; every wave is done with BB
+        chunk_barrier(c == cb);  // chunk c is in BA; every wave is done with BB
         compute(BA, c, BB, c + 1 < ce);
         if (c + 1 >= ce)
             break;
-        dma_barrier();
+        chunk_barrier(false);
         compute(BB, c + 1, BA, c + 2 < ce);
     }
 
