@@ -26,9 +26,13 @@ FAST_NAME = "gdn_fast"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU ops (v_pk_*_f32).
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs. With one wave per SIMD (the 4-wave
+# prefill scan) the register budget is 512 and the compiler otherwise parks MFMA results in
+# AGPRs, paying ~140 v_accvgpr copies per chunk (that scan: 5 % of a 16-sequence prefill).
 HIPCC_FLAGS = [
     "-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
 
