@@ -197,6 +197,10 @@ constexpr int kJobResume = 3;  // from S_in(1) and (steps) chain steps; outputs;
 // * M_s: LDS image of M_s^T split into bf16 hi units (0 .. 2047) then lo units; unit
 //   16 j + (cu ^ kswz(j)) holds M_s[8 cu .. 8 cu + 7][j].
 constexpr int64_t kSlotFloats = 128 * 128;
+// Job entry: {sequence, kind, first chunk, end chunk, slot, chain steps, last, the sequence's
+// first token, length and first chunk, 0 ...}: a scan workgroup reads what it needs in one
+// round of loads, issued together with the job count's.
+constexpr int kJobInts = 16;
 constexpr int kMtUnits = 2048;
 constexpr int kSegMinChunks = 4;            // shortest segment (before balancing)
 constexpr int kSegMaxG = 16;                // segments per sequence at most
@@ -217,9 +221,9 @@ struct PlanArgs {
     int32_t *seq_rank;
     bf16_t *out;
     int64_t o_st, o_sh;
-    // segments (seg_G >= 3): at most seg_G segments per sequence; job entries of 8 ints
-    // {sequence, kind, first chunk, end chunk, slot, chain steps, last}, pass A from
-    // jobs[0], pass C from jobs[8 seg_capA]; counts in header[1], header[2]
+    // segments (seg_G >= 3): at most seg_G segments per sequence; job entries of kJobInts
+    // ints, pass A from jobs[0], pass C from jobs[kJobInts seg_capA]; counts in header[1],
+    // header[2]
     int seg_G, seg_capA;
     int32_t *jobs;
 };
@@ -258,7 +262,7 @@ __device__ __forceinline__ float wave_max_nonneg(float x)
 // slots q .. q + G - 2 of a cut sequence hold S_in(1) and M_s, R_s of the middle segments
 // s (slot q + s - 1).
 __device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const int32_t *first,
-                                 const int32_t *len, int lane)
+                                 const int32_t *tok0, const int32_t *len, int lane)
 {
     constexpr float w = kSegFirstWeight, h = 0.5f * kSegChainChunks;
     const bool act = lane < p.N;
@@ -344,15 +348,12 @@ __device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const 
               totC = (int)__builtin_amdgcn_readlane((int)iC, 63);
     int oF = (int)iF - firstA, oM = totF + (int)iM - mapsA, oC = p.seg_capA + (int)iC - passC;
     const int q = (int)iS - slots;
+    const int t0n = act ? tok0[n] : 0, lenn = act ? len[n] : 0, c0n = act ? first[n] : 0;
     auto put = [&](int idx, int kind, int cb, int ce, int slot, int steps, int last) {
-        int32_t *e = p.jobs + 8 * idx;
-        e[0] = n;
-        e[1] = kind;
-        e[2] = cb;
-        e[3] = ce;
-        e[4] = slot;
-        e[5] = steps;
-        e[6] = last;
+        int4 *e = (int4 *)(p.jobs + kJobInts * idx);
+        e[0] = int4{n, kind, cb, ce};
+        e[1] = int4{slot, steps, last, t0n};
+        e[2] = int4{lenn, c0n, 0, 0};
     };
     if (act) {
         if (whole) {
@@ -432,9 +433,8 @@ struct ScanArgs {
     const int32_t *header, *seq_chunk0, *seq_tok0, *seq_len, *seq_rank;
     const char *records;
     int HQK, HV, ratio, ngroups;
-    // Segment jobs (jobs != nullptr): the grid walks entries jobs[8 (job_first + e)] =
-    // {sequence, kind, first chunk, end chunk, slot, chain steps, last} for
-    // e < header[njob_idx] instead of whole sequences. Slot buffers hold one 128 x 128
+    // Segment jobs (jobs != nullptr): the grid walks entries jobs[kJobInts (job_first + e)]
+    // for e < header[njob_idx] instead of whole sequences. Slot buffers hold one 128 x 128
     // fp32 matrix per (slot, v-head): S_in(1) (seg_sin), R_s (seg_r), or M_s as bf16 hi /
     // lo units (seg_mt, kMtUnits).
     const int32_t *jobs;

@@ -66,7 +66,7 @@ Layout layout(int64_t T, int64_t N, int64_t HV)
     if (L.G > 1) {
         const int64_t slot_bytes = N * (L.G - 1) * HV * gdn::kSlotFloats * 4;
         L.jobs = align256(o);
-        o = L.jobs + (L.capA + L.capC) * 8 * 4;
+        o = L.jobs + (L.capA + L.capC) * gdn::kJobInts * 4;
         L.seg_sin = align256(o);
         L.seg_r = L.seg_sin + slot_bytes;
         L.seg_mt = L.seg_r + slot_bytes;

@@ -108,7 +108,7 @@ __device__ __forceinline__ void self_plan(const PrepArgs &p, PrepSmem<VH> &sm, i
             q.header[0] = sm.s_total;
         }
         if (q.seg_G >= 3)  // every lane of the wave takes part
-            plan_jobs(q, order, sm.s_first, sm.s_len, l);
+            plan_jobs(q, order, sm.s_first, sm.s_t0, sm.s_len, l);
     }
     const int g0 = sm.s_g0, g1 = sm.s_g1, gap = g0 + (q.T - g1);
     if (gap > 0) {

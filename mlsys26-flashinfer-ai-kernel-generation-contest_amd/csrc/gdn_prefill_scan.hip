@@ -45,20 +45,23 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
         return;
     int n, tok0, len, c0, kind = kJobFirst, cb = 0, ce = 0x7fffffff, q = -1, steps = 0, last = 0;
     if constexpr (SEG) {
+        // the grid covers the job table's capacity, so the entry exists even past the job
+        // count, and both load together
         const int e = grp / p.HQK;
+        const int4 *je = (const int4 *)(p.jobs + kJobInts * (p.job_first + e));
+        const int4 j0 = je[0], j1 = je[1], j2 = je[2];
         if (e >= p.header[p.njob_idx])
             return;
-        const int32_t *je = p.jobs + 8 * (p.job_first + e);
-        n = je[0];
-        kind = je[1];
-        cb = je[2];
-        ce = je[3];
-        q = je[4];
-        steps = je[5];
-        last = je[6];
-        tok0 = p.seq_tok0[n];
-        len = p.seq_len[n];
-        c0 = p.seq_chunk0[n];
+        n = j0.x;
+        kind = j0.y;
+        cb = j0.z;
+        ce = j0.w;
+        q = j1.x;
+        steps = j1.y;
+        last = j1.z;
+        tok0 = j1.w;
+        len = j2.x;
+        c0 = j2.y;
     } else {
         const int4 r = *(const int4 *)(p.seq_rank + 4 * (grp / p.HQK));
         n = r.x;
