@@ -29,10 +29,14 @@ ARCH = "gfx950"
 # -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs. With one wave per SIMD (the 4-wave
 # prefill scan) the register budget is 512 and the compiler otherwise parks MFMA results in
 # AGPRs, paying ~140 v_accvgpr copies per chunk (that scan: 5 % of a 16-sequence prefill).
+# -amdgpu-sched-strategy=max-memory-clause: bit-identical results, measured ~1 % faster on
+# MI355X across decode (B=64 42.67 -> 42.35 us) and prefill (8172 tokens 108.6 -> 107.6 us,
+# 1 x 4096 99.0 -> 98.1 us; 21 interleaved trials), and the prep kernel no longer spills.
 HIPCC_FLAGS = [
     "-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    "-mllvm", "-amdgpu-sched-strategy=max-memory-clause",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
 
