@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from gdn_hip import gdn_decode, gdn_prefill
+from gdn_hip import _lib, gdn_decode, gdn_prefill, release_workspace
 from gdn_hip.inputs import prefill_inputs, varlen_lengths, with_extreme_gates
 from gdn_hip.parity import check_output, check_state
 from oracle import gdn_oracle as O
@@ -157,6 +157,54 @@ def test_prefill_resume_split(dev):
                          g.dt_bias, g.b[m:], cu2, g.scale)
     torch.cuda.synchronize()
     _check(torch.cat([o1, o2]), s2, ref_o, ref_s, "resume vs oracle")
+
+
+def test_prefill_records_past_2gib(dev):
+    """Maximum sizes: one 327,680-token sequence at 32 v-heads, whose workspace records
+    (5,121 chunks x 32 v-heads x 16 KB = 2.7 GB) reach past 2^31 bytes, against the same
+    sequence prefilled as five chained 65,536-token calls (0.5 GB of records each, the
+    state handed from call to call). The two runs plan and cut the sequence differently,
+    so they agree to rounding; an offset truncated to 32 bits in the large run would read
+    or write the wrong records. Inputs are drawn on the GPU and compared there (the oracle
+    would need ~0.7 TFLOP in fp64); mild decay keeps earlier chunks' states significant."""
+    T, piece, hqk, hv = 5 << 16, 1 << 16, 2, 32
+    g = torch.Generator(device=dev)
+    g.manual_seed(61)
+    unit = lambda *s: torch.nn.functional.normalize(  # noqa: E731
+        torch.randn(*s, generator=g, device=dev), dim=-1).to(torch.bfloat16)
+    q, k = unit(T, hqk, 128), unit(T, hqk, 128)
+    v = torch.randn(T, hv, 128, generator=g, device=dev).to(torch.bfloat16)
+    a = torch.randn(T, hv, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(T, hv, generator=g, device=dev).to(torch.bfloat16)
+    A_log = -6.0 + 3.0 * torch.rand(hv, generator=g, device=dev)
+    dt_bias = torch.rand(hv, generator=g, device=dev) * 2.0 - 1.0
+    state = torch.randn(1, hv, 128, 128, generator=g, device=dev) * 0.05
+    scale = 128 ** -0.5
+    ws = _lib.load().gdn_prefill_workspace_size(T, 1, hqk, hv, 128)
+    print(f"[{T} tokens] whole-sequence run, workspace {ws / 2**30:.2f} GiB", flush=True)
+    assert ws > (1 << 31)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
+    o_full, s_full = gdn_prefill(q, k, v, state, A_log, a, dt_bias, b, cu, scale)
+    torch.cuda.synchronize()
+    cu_p = torch.tensor([0, piece], dtype=torch.int32, device=dev)
+    s = state
+    outs = []
+    for i in range(T // piece):
+        sl = slice(i * piece, (i + 1) * piece)
+        o, s = gdn_prefill(q[sl], k[sl], v[sl], s, A_log, a[sl], dt_bias, b[sl], cu_p, scale)
+        outs.append(o)
+    torch.cuda.synchronize()
+    # the output bar of gdn_hip.parity (both-condition rule), evaluated on the device
+    x, y = o_full.float(), torch.cat(outs).float()
+    d = (x - y).abs()
+    nfail = int(((d > 1e-2) & (d > 1e-2 * y.abs())).sum())
+    vs = check_state(s_full, s)
+    print(f"[{T} tokens] whole vs chained: output max_abs={float(d.max()):.3e} fail={nfail} | "
+          f"state {vs}", flush=True)
+    assert nfail == 0 and torch.isfinite(x).all()
+    assert vs.ok
+    del x, y, d, o_full, outs, q, k, v
+    release_workspace()
 
 
 @pytest.mark.parametrize("gates", ["strong", "mild"])
