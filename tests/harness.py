@@ -19,7 +19,7 @@ the reference's drivers and their external harness do for this path:
 * the scoring gate: any failing workload zeroes that kernel's score
   (computer_track_scores_local.py:157-158).
 
-    python tests/harness.py [--out harness.json] [--quick]
+    python tests/harness.py [--out harness.json] [--quick] [--filter SUBSTR]
 """
 from __future__ import annotations
 
@@ -147,6 +147,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=None)
     ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--filter", default="",
+                    help="run only workloads whose '<definition>/<workload>' contains this")
     args = ap.parse_args()
     if not torch.cuda.is_available():
         print("harness: no HIP device", file=sys.stderr)
@@ -154,6 +156,8 @@ def main():
     dev = torch.device("cuda", 0)
     results = {}
     for defn, name, kind, inp in workloads(args.quick):
+        if args.filter not in f"{defn}/{name}":
+            continue
         print(f"[harness] {defn} {name} ...", flush=True)
         rec = run_workload(kind, inp, dev)
         results.setdefault(defn, {})[name] = rec
