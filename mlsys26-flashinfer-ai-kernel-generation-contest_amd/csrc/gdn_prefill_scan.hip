@@ -29,46 +29,74 @@ namespace gdn {
 // FUSED (NW == 8, whole sequences): the workgroup has 4 more waves, the prep waves, which
 // build chunk c + 1's K, Q (copies), T', P' and gate area in the other chunk buffer while
 // the 8 scan waves process chunk c; the scan waves copy only V. No records are read.
-template <int NW, bool SEG, bool FUSED = false>
-__device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, ScanBuf<NW> &BB,
-                                          FusedPrepScratch *ps = nullptr)
+// A scan workgroup's job: its (sequence or segment job, q/k head) group grp, its place wi
+// among the group's workgroups, and the job's sequence, kind and chunk range.
+struct ScanJob {
+    int grp, wi, n, tok0, len, c0, kind, cb, ce, q, steps, last;
+};
+
+// Finds this workgroup's job (SEG: in the segment job table); false when it has none.
+template <int NW, bool SEG>
+__device__ __forceinline__ bool scan_job(const ScanArgs &p, ScanJob &j)
 {
-    static_assert(!FUSED || (NW == 8 && !SEG), "the fused kernel scans whole sequences, 8 waves");
     constexpr int TPH = 8 / NW;  // workgroups per (sequence, v-head)
     // Workgroups of one (sequence, q/k head) share K, Q through L2: one XCD for them all
     // (workgroup ids are dealt to the 8 XCDs round-robin).
     const int pid = blockIdx.x, xcd = pid & 7, slot = pid >> 3;
     const int gsz = TPH * p.ratio;
-    const int wi = slot % gsz;
-    const int grp = (slot / gsz) * 8 + xcd;
-    if (grp >= p.ngroups)
-        return;
-    int n, tok0, len, c0, kind = kJobFirst, cb = 0, ce = 0x7fffffff, q = -1, steps = 0, last = 0;
+    j.wi = slot % gsz;
+    j.grp = (slot / gsz) * 8 + xcd;
+    if (j.grp >= p.ngroups)
+        return false;
+    j.kind = kJobFirst;
+    j.cb = 0;
+    j.ce = 0x7fffffff;
+    j.q = -1;
+    j.steps = 0;
+    j.last = 0;
     if constexpr (SEG) {
         // the grid covers the job table's capacity, so the entry exists even past the job
         // count, and both load together
-        const int e = grp / p.HQK;
+        const int e = j.grp / p.HQK;
         const int4 *je = (const int4 *)(p.jobs + kJobInts * (p.job_first + e));
         const int4 j0 = je[0], j1 = je[1], j2 = je[2];
         if (e >= p.header[p.njob_idx])
-            return;
-        n = j0.x;
-        kind = j0.y;
-        cb = j0.z;
-        ce = j0.w;
-        q = j1.x;
-        steps = j1.y;
-        last = j1.z;
-        tok0 = j1.w;
-        len = j2.x;
-        c0 = j2.y;
+            return false;
+        j.n = j0.x;
+        j.kind = j0.y;
+        j.cb = j0.z;
+        j.ce = j0.w;
+        j.q = j1.x;
+        j.steps = j1.y;
+        j.last = j1.z;
+        j.tok0 = j1.w;
+        j.len = j2.x;
+        j.c0 = j2.y;
     } else {
-        const int4 r = *(const int4 *)(p.seq_rank + 4 * (grp / p.HQK));
-        n = r.x;
-        tok0 = r.y;
-        len = r.z;
-        c0 = r.w;
+        const int4 r = *(const int4 *)(p.seq_rank + 4 * (j.grp / p.HQK));
+        j.n = r.x;
+        j.tok0 = r.y;
+        j.len = r.z;
+        j.c0 = r.w;
     }
+    return true;
+}
+
+// SEG: the body handles every segment job kind; otherwise only jobs from the initial state
+// with outputs into new_state (whole sequences), with none of the segment code compiled in.
+// INST tags an instance: the whole-sequence body inside a segment kernel is instance 1, so
+// each instance is used by one kernel only (hipcc's host pass rejects a second kernel's use
+// of an instance of this device-only template: "substitution failure").
+template <int NW, bool SEG, bool FUSED = false, int INST = 0>
+__device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job, ScanBuf<NW> &BA,
+                                          ScanBuf<NW> &BB, FusedPrepScratch *ps = nullptr)
+{
+    static_assert(!FUSED || (NW == 8 && !SEG), "the fused kernel scans whole sequences, 8 waves");
+    constexpr int TPH = 8 / NW;  // workgroups per (sequence, v-head)
+    const int grp = job.grp, wi = job.wi, n = job.n, tok0 = job.tok0, len = job.len,
+              c0 = job.c0, kind = SEG ? job.kind : kJobFirst, cb = SEG ? job.cb : 0,
+              q = SEG ? job.q : -1, steps = SEG ? job.steps : 0, last = SEG ? job.last : 0;
+    int ce = SEG ? job.ce : 0x7fffffff;
     const int g = grp % p.HQK;
     const int h = g * p.ratio + wi / TPH;
     const int v0 = (wi % TPH) * 16 * NW;
@@ -704,25 +732,62 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, ScanBuf<NW> &BA, Sc
     }
 }
 
+// The kernel's argument block through a pointer taken from the kernarg segment register and
+// passed through an empty asm, so the compiler cannot prove it equal to the one behind the
+// kernel parameter. A body given it keeps its own argument loads: with both bodies in one
+// kernel on one pointer, the compiler merged their loads of the same fields above the branch
+// and kept them live through both loops (scan4 segment kernel: 102 SGPRs spilled instead of
+// 19; the segment passes ran up to 3 % slower).
+__device__ __forceinline__ const ScanArgs &fresh_kernel_args()
+{
+    typedef const ScanArgs __attribute__((address_space(4))) *KArgs;
+    KArgs kp = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kp));
+    return *(const ScanArgs *)kp;
+}
+
+// A whole sequence listed in a segment job table (kJobFirst without a slot: from the initial
+// state, outputs, final state into new_state) takes the whole-sequence body, whose loop
+// carries none of the segment code (measured on MI355X, bit-identical: the qk4_v8 prefills
+// of 8 sequences, all whole or mixed with cut ones, 44.4 -> 40.9 and 54.9 -> 49.9 us).
+template <int NW, bool SEG>
+__device__ __forceinline__ void scan_kernel_body(const ScanArgs &p, ScanBuf<NW> &BA,
+                                                 ScanBuf<NW> &BB)
+{
+    ScanJob job;
+    if (!scan_job<NW, SEG>(p, job))
+        return;
+    if constexpr (SEG) {
+        if (job.kind == kJobFirst && job.q < 0 && job.cb == 0) {
+            scan_body<NW, false, false, 1>(fresh_kernel_args(), job, BA, BB);
+            return;
+        }
+    }
+    scan_body<NW, SEG>(p, job, BA, BB);
+}
+
 template <bool SEG>
 __global__ __launch_bounds__(512) void gdn_prefill_scan8_kernel(ScanArgs p)
 {
     __shared__ ScanBuf<8> bufA, bufB;
-    scan_body<8, SEG>(p, bufA, bufB);
+    scan_kernel_body<8, SEG>(p, bufA, bufB);
 }
 
 template <bool SEG>
 __global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p)
 {
     __shared__ ScanBuf<4> bufA, bufB;
-    scan_body<4, SEG>(p, bufA, bufB);
+    scan_kernel_body<4, SEG>(p, bufA, bufB);
 }
 
 __global__ __launch_bounds__(768) void gdn_prefill_fused_kernel(ScanArgs p)
 {
     __shared__ ScanBuf<8> bufA, bufB;
     __shared__ FusedPrepScratch ps;
-    scan_body<8, false, true>(p, bufA, bufB, &ps);
+    ScanJob job;
+    if (!scan_job<8, false>(p, job))
+        return;
+    scan_body<8, false, true>(p, job, bufA, bufB, &ps);
 }
 
 template __global__ void gdn_prefill_scan8_kernel<false>(ScanArgs p);
