@@ -84,10 +84,12 @@ __device__ __forceinline__ bool scan_job(const ScanArgs &p, ScanJob &j)
 
 // SEG: the body handles every segment job kind; otherwise only jobs from the initial state
 // with outputs into new_state (whole sequences), with none of the segment code compiled in.
+// OUTS (segment bodies): 1 compiles the body for jobs with outputs (kJobFirst, kJobResume),
+// 0 for the state maps (kJobZero, kJobIdent), so the loop carries no run-time output test.
 // INST tags an instance: the whole-sequence body inside a segment kernel is instance 1, so
 // each instance is used by one kernel only (hipcc's host pass rejects a second kernel's use
 // of an instance of this device-only template: "substitution failure").
-template <int NW, bool SEG, bool FUSED = false, int INST = 0>
+template <int NW, bool SEG, bool FUSED = false, int INST = 0, int OUTS = -1>
 __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job, ScanBuf<NW> &BA,
                                           ScanBuf<NW> &BB, FusedPrepScratch *ps = nullptr)
 {
@@ -103,8 +105,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
     // records exist only for chunk ids < header[0] (see the plan kernel's clamp)
     const int nck = min((len + kC - 1) / kC, max(p.header[0] - c0, 0));
     ce = min(ce, nck);
-    const bool do_out = kind == kJobFirst || kind == kJobResume;
-    const bool vzero = kind == kJobIdent;
+    const bool do_out = OUTS >= 0 ? OUTS == 1 : kind == kJobFirst || kind == kJobResume;
+    const bool vzero = OUTS != 1 && kind == kJobIdent;
 
     // w is wave-uniform: LDS copy destinations (M0) are then scalar arithmetic
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
@@ -734,10 +736,10 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
 
 // The kernel's argument block through a pointer taken from the kernarg segment register and
 // passed through an empty asm, so the compiler cannot prove it equal to the one behind the
-// kernel parameter. A body given it keeps its own argument loads: with both bodies in one
-// kernel on one pointer, the compiler merged their loads of the same fields above the branch
-// and kept them live through both loops (scan4 segment kernel: 102 SGPRs spilled instead of
-// 19; the segment passes ran up to 3 % slower).
+// kernel parameter or another call's. A body given it keeps its own argument loads: with
+// several bodies in one kernel on one pointer, the compiler merged their loads of the same
+// fields above the branch and kept them live through every loop (scan4 segment kernel with
+// two bodies: 102 SGPRs spilled instead of 26; the segment passes ran up to 3 % slower).
 __device__ __forceinline__ const ScanArgs &fresh_kernel_args()
 {
     typedef const ScanArgs __attribute__((address_space(4))) *KArgs;
@@ -746,10 +748,13 @@ __device__ __forceinline__ const ScanArgs &fresh_kernel_args()
     return *(const ScanArgs *)kp;
 }
 
-// A whole sequence listed in a segment job table (kJobFirst without a slot: from the initial
-// state, outputs, final state into new_state) takes the whole-sequence body, whose loop
-// carries none of the segment code (measured on MI355X, bit-identical: the qk4_v8 prefills
-// of 8 sequences, all whole or mixed with cut ones, 44.4 -> 40.9 and 54.9 -> 49.9 us).
+// A segment kernel holds three bodies, each on its own argument pointer: a whole sequence
+// listed in the job table (kJobFirst without a slot: from the initial state, outputs, final
+// state into new_state) takes the whole-sequence body, whose loop carries none of the segment
+// code; segment jobs with outputs and state maps take one body each. Measured on MI355X,
+// bit-identical against one segment body for every job: the qk4_v8 prefills of 8 sequences
+// (all whole, or mixed with cut ones) 44.4 -> 40.9 and 54.9 -> 49.9 us; 1 x 4096 at 32
+// v-heads 98.4 -> 93.0 us.
 template <int NW, bool SEG>
 __device__ __forceinline__ void scan_kernel_body(const ScanArgs &p, ScanBuf<NW> &BA,
                                                  ScanBuf<NW> &BB)
@@ -760,10 +765,14 @@ __device__ __forceinline__ void scan_kernel_body(const ScanArgs &p, ScanBuf<NW> 
     if constexpr (SEG) {
         if (job.kind == kJobFirst && job.q < 0 && job.cb == 0) {
             scan_body<NW, false, false, 1>(fresh_kernel_args(), job, BA, BB);
-            return;
+        } else if (job.kind == kJobFirst || job.kind == kJobResume) {
+            scan_body<NW, true, false, 0, 1>(fresh_kernel_args(), job, BA, BB);
+        } else {
+            scan_body<NW, true, false, 0, 0>(fresh_kernel_args(), job, BA, BB);
         }
+    } else {
+        scan_body<NW, SEG>(p, job, BA, BB);
     }
-    scan_body<NW, SEG>(p, job, BA, BB);
 }
 
 template <bool SEG>
