@@ -85,7 +85,9 @@ __device__ __forceinline__ bool scan_job(const ScanArgs &p, ScanJob &j)
 // SEG: the body handles every segment job kind; otherwise only jobs from the initial state
 // with outputs into new_state (whole sequences), with none of the segment code compiled in.
 // OUTS (segment bodies): 1 compiles the body for jobs with outputs (kJobFirst, kJobResume),
-// 0 for the state maps (kJobZero, kJobIdent), so the loop carries no run-time output test.
+// 0 for value-row maps (kJobZero), 2 for identity-row maps (kJobIdent), so the loop carries
+// no run-time test of the job kind. The maps copy neither Q nor P' (no outputs), and the
+// identity maps no V (V = 0).
 // INST tags an instance: the whole-sequence body inside a segment kernel is instance 1, so
 // each instance is used by one kernel only (hipcc's host pass rejects a second kernel's use
 // of an instance of this device-only template: "substitution failure").
@@ -106,7 +108,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
     const int nck = min((len + kC - 1) / kC, max(p.header[0] - c0, 0));
     ce = min(ce, nck);
     const bool do_out = OUTS >= 0 ? OUTS == 1 : kind == kJobFirst || kind == kJobResume;
-    const bool vzero = OUTS != 1 && kind == kJobIdent;
+    const bool vzero = OUTS == 2 || (OUTS < 0 && kind == kJobIdent);
 
     // w is wave-uniform: LDS copy destinations (M0) are then scalar arithmetic
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
@@ -216,13 +218,19 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
         if (NW * i < 16) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.k, (GDN_LDS void *)&B.K[64 * win], 16, woff[i], 0, 0, 0);
         } else if (NW * i < 32) {
+            if (OUTS == 0 || OUTS == 2)  // state maps read neither Q nor P'
+                return;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.q, (GDN_LDS void *)&B.Q[64 * (win - 16)], 16, woff[i], 0, 0, 0);
         } else if (NW * i < 32 + VWIN) {
+            if (OUTS == 2)  // identity rows: V = 0
+                return;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.v, (GDN_LDS void *)&B.V[64 * (win - 32)], 16, woff[i], 0, 0, 0);
         } else if (win < NWIN) {
             const int r = win - 32 - VWIN;
             if (r < 18) {
                 const int mt = r / 6, pr = r % 6, b = pr == 0 ? 0 : (pr == 1 ? 2 : pr + 2);
+                if ((OUTS == 0 || OUTS == 2) && mt == 2)
+                    return;
                 u32x4 *dst = mt == 2 ? &B.P[64 * b] : &B.T[mt][64 * b];
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.r, (GDN_LDS void *)dst, 16, woff[i], 0, 0, 0);
             } else {
@@ -748,13 +756,13 @@ __device__ __forceinline__ const ScanArgs &fresh_kernel_args()
     return *(const ScanArgs *)kp;
 }
 
-// A segment kernel holds three bodies, each on its own argument pointer: a whole sequence
+// A segment kernel holds four bodies, each on its own argument pointer: a whole sequence
 // listed in the job table (kJobFirst without a slot: from the initial state, outputs, final
 // state into new_state) takes the whole-sequence body, whose loop carries none of the segment
-// code; segment jobs with outputs and state maps take one body each. Measured on MI355X,
-// bit-identical against one segment body for every job: the qk4_v8 prefills of 8 sequences
-// (all whole, or mixed with cut ones) 44.4 -> 40.9 and 54.9 -> 49.9 us; 1 x 4096 at 32
-// v-heads 98.4 -> 93.0 us.
+// code; segment jobs with outputs and the two kinds of state map take one body each.
+// Measured on MI355X, bit-identical against one segment body for every job: the qk4_v8
+// prefills of 8 sequences (all whole, or mixed with cut ones) 44.4 -> 40.9 and 54.9 -> 49.9
+// us; 1 x 4096 at 32 v-heads 98.4 -> 91.9 us.
 template <int NW, bool SEG>
 __device__ __forceinline__ void scan_kernel_body(const ScanArgs &p, ScanBuf<NW> &BA,
                                                  ScanBuf<NW> &BB)
@@ -767,8 +775,10 @@ __device__ __forceinline__ void scan_kernel_body(const ScanArgs &p, ScanBuf<NW> 
             scan_body<NW, false, false, 1>(fresh_kernel_args(), job, BA, BB);
         } else if (job.kind == kJobFirst || job.kind == kJobResume) {
             scan_body<NW, true, false, 0, 1>(fresh_kernel_args(), job, BA, BB);
-        } else {
+        } else if (job.kind == kJobZero) {
             scan_body<NW, true, false, 0, 0>(fresh_kernel_args(), job, BA, BB);
+        } else {
+            scan_body<NW, true, false, 0, 2>(fresh_kernel_args(), job, BA, BB);
         }
     } else {
         scan_body<NW, SEG>(p, job, BA, BB);
