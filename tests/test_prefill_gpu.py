@@ -299,13 +299,16 @@ def test_prefill_segments_mixed(dev, lens, hqk, hv):
 @pytest.mark.parametrize("lens,plan", [
     (varlen_lengths(8, seed=7), (0, 8)),  # 12, 11, 11, 8, 8, 7, 5, 2 chunks: no cut pays off
     ([4096, 700, 650], (9, 7)),           # 64 chunks in 6 segments; 11-chunk ones whole in C
+    ([3000, 200, 150, 100], (10, 4)),     # 47 chunks in 5 segments; the short ones whole in A
 ])
 def test_prefill_segment_planner(dev, lens, plan):
     """Segment plans on few sequences (qk4_v8 heads; mild decay, so every chained state
     carries into the next segment). Sequences of similar length all run whole in pass C
     with pass A empty; a long sequence is cut into segments while the short ones run whole
-    in pass C beside its resumed segments. The job counts the planner wrote (workspace
-    header: pass A, pass C) name the plan taken."""
+    in pass C beside its resumed segments, or in pass A beside its segment 0 and state maps.
+    Each segment kernel then runs every body it holds (whole sequence, segment with
+    outputs, both state maps). The job counts the planner wrote (workspace header: pass A,
+    pass C) name the plan taken."""
     from gdn_hip import _lib
     from gdn_hip.api import _prefill_marshal
     inp = prefill_inputs(lens, hqk=4, hv=8, seed=59, with_state=True, gates="mild",
