@@ -300,6 +300,8 @@ def test_prefill_segments_mixed(dev, lens, hqk, hv):
     (varlen_lengths(8, seed=7), (0, 8)),  # 12, 11, 11, 8, 8, 7, 5, 2 chunks: no cut pays off
     ([4096, 700, 650], (9, 7)),           # 64 chunks in 6 segments; 11-chunk ones whole in C
     ([3000, 200, 150, 100], (10, 4)),     # 47 chunks in 5 segments; the short ones whole in A
+    # 10-12 chunks each: no cut pays off; ten sequences make pass C the 8-wave kernel
+    ([720, 700, 705, 690, 680, 660, 650, 640, 600, 710], (0, 10)),
 ])
 def test_prefill_segment_planner(dev, lens, plan):
     """Segment plans on few sequences (qk4_v8 heads; mild decay, so every chained state
