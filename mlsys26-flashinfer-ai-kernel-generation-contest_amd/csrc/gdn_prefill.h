@@ -222,9 +222,12 @@ struct PlanArgs {
     bf16_t *out;
     int64_t o_st, o_sh;
     // segments (seg_G >= 3): at most seg_G segments per sequence; job entries of kJobInts
-    // ints, pass A from jobs[0], pass C from jobs[kJobInts seg_capA]; counts in header[1],
-    // header[2]
-    int seg_G, seg_capA;
+    // ints, pass A from jobs[0], pass C from jobs[kJobInts seg_capA]; counts in header[1]
+    // (pass A) and header[2] (pass C). seg_c4 > 0: pass C is launched twice, with 4 and with
+    // 8 waves per workgroup; a plan with at most seg_c4 pass-C jobs (128 (job, v-head) pairs)
+    // counts them in header[2] for the 4-wave launch, a larger one in header[3] for the
+    // 8-wave launch, and the other launch finds no job.
+    int seg_G, seg_capA, seg_c4;
     int32_t *jobs;
 };
 
@@ -371,8 +374,10 @@ __device__ inline void plan_jobs(const PlanArgs &p, const int32_t *order, const 
         }
     }
     if (lane == 0) {
+        const bool c8 = p.seg_c4 > 0 && totC > p.seg_c4;
         p.header[1] = totF + totM;
-        p.header[2] = totC;
+        p.header[2] = c8 ? 0 : totC;
+        p.header[3] = c8 ? totC : 0;
     }
 }
 

@@ -212,6 +212,12 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     const bool fused = G == 1 && p->variant == 3;
     pa.seg_G = G;
     pa.seg_capA = (int)L.capA;
+    // Pass C: the 4-wave kernel (two workgroups per (job, v-head), spread over twice the CUs)
+    // when its job capacity fits 128 pairs; otherwise both kernels are launched and the
+    // planner gives the jobs to the 4-wave one whenever the plan's pass C fits 128 pairs
+    // (every plan that cuts nothing, for one), else to the 8-wave one.
+    const bool c4_only = L.capC * HV <= 128;
+    pa.seg_c4 = G > 1 && !c4_only ? (int)(128 / HV) : 0;
     pa.jobs = G > 1 ? (int32_t *)(ws + L.jobs) : nullptr;
     // Up to 64 sequences the prep kernel plans for itself (one dependent launch fewer:
     // the plan kernel's ~5 us sat on the critical path, mostly cu_seqlens load latency).
@@ -355,7 +361,11 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
             // the last segment's final state is new_state
             sa.job_first = (int)L.capA;
             sa.njob_idx = 2;
-            rc = scan(L.capC, L.capC * HV <= 128);
+            rc = scan(c4_only ? L.capC : pa.seg_c4, true);
+            if (rc == 0 && !c4_only) {
+                sa.njob_idx = 3;
+                rc = scan(L.capC, false);
+            }
         } else {
             rc = scan(N, nw4);
         }

@@ -297,11 +297,14 @@ def test_prefill_segments_mixed(dev, lens, hqk, hv):
 
 
 @pytest.mark.parametrize("lens,plan", [
-    (varlen_lengths(8, seed=7), (0, 8)),  # 12, 11, 11, 8, 8, 7, 5, 2 chunks: no cut pays off
-    ([4096, 700, 650], (9, 7)),           # 64 chunks in 6 segments; 11-chunk ones whole in C
-    ([3000, 200, 150, 100], (10, 4)),     # 47 chunks in 5 segments; the short ones whole in A
-    # 10-12 chunks each: no cut pays off; ten sequences make pass C the 8-wave kernel
-    ([720, 700, 705, 690, 680, 660, 650, 640, 600, 710], (0, 10)),
+    (varlen_lengths(8, seed=7), (0, 8, 0)),  # 12, 11, 11, 8, 8, 7, 5, 2 chunks: no cut pays off
+    ([4096, 700, 650], (9, 7, 0)),           # 64 chunks in 6 segments; 11-chunk ones whole in C
+    ([3000, 200, 150, 100], (10, 4, 0)),     # 47 chunks in 5 segments; the short ones whole in A
+    # ten sequences: pass C launched with 4 and with 8 waves. 10-12 chunks each: nothing is
+    # cut, and the ten whole jobs fit the 4-wave launch
+    ([720, 700, 705, 690, 680, 660, 650, 640, 600, 710], (0, 10, 0)),
+    # 44-50 chunks each: all cut in 3 segments, 20 resumed segments for the 8-wave launch
+    ([3000, 2900, 3100, 2950, 3050, 2800, 3200, 2850, 3150, 2990], (30, 0, 20)),
 ])
 def test_prefill_segment_planner(dev, lens, plan):
     """Segment plans on few sequences (qk4_v8 heads; mild decay, so every chained state
@@ -310,7 +313,7 @@ def test_prefill_segment_planner(dev, lens, plan):
     in pass C beside its resumed segments, or in pass A beside its segment 0 and state maps.
     Each segment kernel then runs every body it holds (whole sequence, segment with
     outputs, both state maps). The job counts the planner wrote (workspace header: pass A,
-    pass C) name the plan taken."""
+    pass C in the 4-wave launch, pass C in the 8-wave launch) name the plan taken."""
     from gdn_hip import _lib
     from gdn_hip.api import _prefill_marshal
     inp = prefill_inputs(lens, hqk=4, hv=8, seed=59, with_state=True, gates="mild",
@@ -324,9 +327,10 @@ def test_prefill_segment_planner(dev, lens, plan):
     rc = _lib.load().gdn_prefill_launch(ctypes.byref(P), ctypes.c_void_p(stream.cuda_stream))
     assert rc == 0, _lib.load().gdn_last_error()
     torch.cuda.synchronize()
-    header = keep[-1][:12].view(torch.int32).cpu().tolist()
-    print(f"[planner {lens[:3]}] pass A jobs {header[1]}, pass C jobs {header[2]}", flush=True)
-    assert (header[1], header[2]) == plan
+    header = keep[-1][:16].view(torch.int32).cpu().tolist()
+    print(f"[planner {lens[:3]}] pass A jobs {header[1]}, pass C jobs {header[2]} (4 waves) "
+          f"{header[3]} (8 waves)", flush=True)
+    assert (header[1], header[2], header[3]) == plan
     _check(out, ns, ref_out, ref_ns, f"planner {plan}")
 
 
