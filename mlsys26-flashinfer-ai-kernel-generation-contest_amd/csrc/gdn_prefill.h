@@ -228,6 +228,10 @@ struct PlanArgs {
     // counts them in header[2] for the 4-wave launch, a larger one in header[3] for the
     // 8-wave launch, and the other launch finds no job.
     int seg_G, seg_capA, seg_c4;
+    // whole_cus > 0 (whole sequences, the 4-wave and the 8-wave scan both launched, this many
+    // CUs): the planner gives the sequences to the 4-wave launch (header[4] = N, header[5] = 0)
+    // when it is the faster, else to the 8-wave launch (header[4] = 0, header[5] = N)
+    int whole_cus;
     int32_t *jobs;
 };
 
@@ -439,7 +443,9 @@ struct ScanArgs {
     const char *records;
     int HQK, HV, ratio, ngroups;
     // Segment jobs (jobs != nullptr): the grid walks entries jobs[kJobInts (job_first + e)]
-    // for e < header[njob_idx] instead of whole sequences. Slot buffers hold one 128 x 128
+    // for e < header[njob_idx] instead of whole sequences. Whole sequences (jobs == nullptr)
+    // with njob_idx > 0: only the sequences of rank < header[njob_idx] are scanned (the
+    // planner hands all or none of them to this launch). Slot buffers hold one 128 x 128
     // fp32 matrix per (slot, v-head): S_in(1) (seg_sin), R_s (seg_r), or M_s as bf16 hi /
     // lo units (seg_mt, kMtUnits).
     const int32_t *jobs;

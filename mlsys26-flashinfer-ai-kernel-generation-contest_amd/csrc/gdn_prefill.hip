@@ -223,6 +223,14 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     // the plan kernel's ~5 us sat on the critical path, mostly cu_seqlens load latency).
     const bool prep_runs = L.nc > 0 && T > 0 && !fused;
     const bool self_plan = prep_runs && N >= 1 && N <= gdn::kSelfPlanMax;
+    // Whole sequences, 129 to 256 (sequence, v-head) pairs: either scan can be the faster,
+    // depending on the longest sequence, which only the device knows. Both are launched
+    // and the self-planning prep kernel gives the sequences to one of them; the other
+    // launch finds none (~1.5-2 us for its up to 512 workgroups, one per CU at a time for
+    // their LDS). Above 256 pairs the 8-wave scan alone (the 4-wave one rarely wins there).
+    const bool whole_dual = G == 1 && p->variant == 0 && self_plan && (int64_t)N * HV > 128 &&
+                            (int64_t)N * HV <= 256;
+    pa.whole_cus = whole_dual ? num_cus(st) : 0;
     gdn_begin_launches();
     int rc = 0;
     if (!self_plan) {
@@ -365,6 +373,13 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
             if (rc == 0 && !c4_only) {
                 sa.njob_idx = 3;
                 rc = scan(L.capC, false);
+            }
+        } else if (whole_dual) {
+            sa.njob_idx = 4;
+            rc = scan(N, true);
+            if (rc == 0) {
+                sa.njob_idx = 5;
+                rc = scan(N, false);
             }
         } else {
             rc = scan(N, nw4);

@@ -109,6 +109,22 @@ __device__ __forceinline__ void self_plan(const PrepArgs &p, PrepSmem<VH> &sm, i
         }
         if (q.seg_G >= 3)  // every lane of the wave takes part
             plan_jobs(q, order, sm.s_first, sm.s_t0, sm.s_len, l);
+        if (q.whole_cus > 0) {
+            // Whole sequences, both scans launched. The 4-wave scan spreads each (sequence,
+            // v-head) over two CUs: a chunk takes ~0.74 of the 8-wave scan's time, but
+            // costs 1.5 times the CU time. It is the faster while its average load per CU
+            // (chunk-times over all jobs) stays below the longest sequence, which bounds
+            // both scans from below (measured on MI355X at load / longest: 0.71 -13 %,
+            // 1.02 -4 %, 1.06 +3 %, 1.27 +6 %); 0.9 leaves the close calls to the 8-wave
+            // scan.
+            const float cmax = wave_max_nonneg((float)nck);
+            const float load4 = 2.f * (float)sm.s_total * (float)q.HO / (float)q.whole_cus;
+            const bool use4 = load4 <= 0.9f * cmax;
+            if (l == 0) {
+                q.header[4] = use4 ? q.N : 0;
+                q.header[5] = use4 ? 0 : q.N;
+            }
+        }
     }
     const int g0 = sm.s_g0, g1 = sm.s_g1, gap = g0 + (q.T - g1);
     if (gap > 0) {

@@ -73,7 +73,11 @@ __device__ __forceinline__ bool scan_job(const ScanArgs &p, ScanJob &j)
         j.len = j2.x;
         j.c0 = j2.y;
     } else {
-        const int4 r = *(const int4 *)(p.seq_rank + 4 * (j.grp / p.HQK));
+        // ranks below ngroups / HQK = N all have an entry: load it with the count
+        const int e = j.grp / p.HQK;
+        const int4 r = *(const int4 *)(p.seq_rank + 4 * e);
+        if (p.njob_idx > 0 && e >= p.header[p.njob_idx])
+            return false;
         j.n = r.x;
         j.tok0 = r.y;
         j.len = r.z;

@@ -334,6 +334,31 @@ def test_prefill_segment_planner(dev, lens, plan):
     _check(out, ns, ref_out, ref_ns, f"planner {plan}")
 
 
+@pytest.mark.parametrize("n,seed,use4", [(20, 4, True), (32, 6, False)])
+def test_prefill_whole_scan_choice(dev, n, seed, use4):
+    """Whole sequences with 129 to 256 (sequence, v-head) pairs: both scans are launched and
+    the prep kernel gives the sequences to the 4-wave one when its load per CU stays below
+    the longest sequence (20 qk4_v8 sequences), else to the 8-wave one (32 sequences). The
+    workspace header holds the counts (4-wave, 8-wave); the results hold the oracle bar."""
+    from gdn_hip import _lib
+    from gdn_hip.api import _prefill_marshal
+    lens = varlen_lengths(n, seed=seed)
+    inp = prefill_inputs(lens, hqk=4, hv=8, seed=seed, with_state=True)
+    ref_out, ref_ns = _oracle(inp)
+    g = inp.to(dev)
+    out = torch.empty((g.q.shape[0], 8, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((n, 8, 128, 128), dtype=torch.float32, device=dev)
+    P, _, _, copy_back, keep, stream = _prefill_marshal(*g.args(), out, ns)
+    assert not copy_back
+    rc = _lib.load().gdn_prefill_launch(ctypes.byref(P), ctypes.c_void_p(stream.cuda_stream))
+    assert rc == 0, _lib.load().gdn_last_error()
+    torch.cuda.synchronize()
+    header = keep[-1][:32].view(torch.int32).cpu().tolist()
+    print(f"[whole scan choice N={n}] 4-wave {header[4]}, 8-wave {header[5]}", flush=True)
+    assert (header[4], header[5]) == ((n, 0) if use4 else (0, n))
+    _check(out, ns, ref_out, ref_ns, f"whole scan choice N={n}")
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_prefill_segment_planner_random(dev, seed):
     """Random mixes in the segment regime (2 to 10 sequences, qk4_v8 heads, N HV 3 <= 256):
