@@ -203,7 +203,8 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     // segments only for the default variant (the tuning variants keep whole sequences)
     const int G = p->variant == 0 ? L.G : 1;
     // Whole sequences: 4 scan waves per workgroup (two workgroups per (sequence, v-head))
-    // when there are at most 128 (sequence, v-head) pairs, else 8. Variants: 1 forces 4
+    // when there are at most 128 (sequence, v-head) pairs, else 8 (129 to 256 pairs: the
+    // device picks, whole_dual below). Variants: 1 forces 4
     // waves, 2 forces 8, 3 runs the fused kernel (8 scan waves and 4 prep waves, no prep
     // pass and no records). The fused kernel is exact but slower on MI355X: the prep
     // waves' per-chunk chain (copies, gates, P' and A, substitution, T chain, ~12k cycles)
