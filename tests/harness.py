@@ -60,7 +60,8 @@ def workloads(quick=False):
                    decode_inputs(B, seed=B)))
     pre4 = [("prefill_varlen8", varlen_lengths(8, seed=7)), ("prefill_1x1024", [1024])]
     if not quick:
-        pre4 += [("prefill_varlen16", varlen_lengths(16, seed=3)), ("prefill_1x4096", [4096])]
+        pre4 += [("prefill_varlen16", varlen_lengths(16, seed=3)), ("prefill_1x4096", [4096]),
+                 ("prefill_varlen24", varlen_lengths(24, seed=5)), ("prefill_1x256", [256])]
     for name, lens in pre4:
         wl.append(("gdn_prefill_qk4_v8_d128_k_last", name, "prefill",
                    prefill_inputs(lens, hqk=4, hv=8, seed=len(lens), with_state=True)))
