@@ -3,6 +3,7 @@
 #include "gdn_prefill.h"
 
 #include <algorithm>
+#include <cmath>
 
 // ------------------------------------------------------------------------- host side
 namespace {
@@ -23,10 +24,19 @@ int seg_count(int64_t T, int64_t N, int64_t HV)
     // (the job planner runs one sequence per lane in the self-planned prep kernel)
     if (T <= 0 || N <= 0 || N > gdn::kSelfPlanMax || N * HV * 3 > 256)
         return 1;
-    int G = 3;
+    int64_t G = 3;
     while (G < gdn::kSegMaxG && N * HV * (2 * (G + 1) - 3) <= 256)
         ++G;
-    return G;
+    // No sequence has more than ceil(T / 64) chunks, and the planner cuts one of c chunks
+    // into at most min(G, c / kSegMinChunks, G*(c)) segments, G* its closed-form optimum
+    // (rising with c; +1 for the device's float rounding). Capacities sized for that count
+    // are tight for a single sequence (1 x 1024 at 8 v-heads: 4 segments instead of 16),
+    // and below 3 no sequence is cut at all: one whole-sequence scan.
+    const int64_t cmax = (T + kChunkH - 1) / kChunkH;
+    const double w = gdn::kSegFirstWeight, h = 0.5 * gdn::kSegChainChunks;
+    const int64_t gs = (int64_t)(1.0 - w + std::sqrt(w * w + w + (double)cmax / h)) + 1;
+    G = std::min({G, cmax / gdn::kSegMinChunks, gs});
+    return G >= 3 ? (int)G : 1;
 }
 
 struct Layout {
@@ -363,7 +373,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
             sa.jobs = pa.jobs;
             sa.job_first = 0;
             sa.njob_idx = 1;
-            rc = scan(L.capA, false);
+            rc = scan(L.capA, L.capA * HV <= 128);
             if (rc)
                 return rc;
             // pass C: outputs of segments 1 .. G - 1, each chaining its entering state first;
