@@ -4,7 +4,9 @@
  * Plain C: raw device pointers, element strides and sizes; no torch types.
  * Every entry point returns 0 on success or a negative GDN_E* code, in which
  * case gdn_last_error() describes the failure (per calling thread; each call clears
- * it first, and drains any HIP error an earlier call left pending). Argument errors
+ * it first). A HIP error that an earlier call left pending on the thread is drained
+ * before the launches, so that it is not blamed on this call, and named in
+ * gdn_last_error() (starting "note:") even when the call succeeds. Argument errors
  * are reported before anything is launched; after GDN_ELAUNCH, kernels launched
  * before the failing one may already have written part of the outputs. Launches are
  * asynchronous on the given stream (a hipStream_t; NULL = the default stream);
@@ -66,7 +68,7 @@ typedef struct gdn_decode_params {
     int32_t num_v_heads; /* a multiple of num_qk_heads, at most 65535 */
     int32_t head_size;   /* D */
     float scale;         /* readout scale; the caller resolves 0 -> 1/sqrt(D) */
-    int32_t variant;     /* kernel variant for tuning sweeps; 0 = tuned default */
+    int32_t variant;     /* must be 0 (the tuned kernel); anything else: GDN_EINVAL */
     const void *q;        int64_t q_stride[4];
     const void *k;        int64_t k_stride[4];
     const void *v;        int64_t v_stride[4];
@@ -104,10 +106,9 @@ typedef struct gdn_prefill_params {
     int32_t head_size;    /* D (must be 128) */
     float scale;
     int32_t cu_seqlens_int64; /* 1: int64 cu_seqlens, 0: int32 */
-    int32_t variant;      /* 0 = tuned default. Tuning variants, all scanning whole
-                             sequences (no segments): 1 / 2 force 4 / 8 scan waves
-                             per workgroup; 3 = fused prep + scan kernel
-                             (bit-identical to 2, slower on MI355X) */
+    int32_t variant;      /* 0 = tuned default. 1 / 2 scan every sequence whole (no
+                             segments) with 4 / 8 scan waves per workgroup;
+                             anything else: GDN_EINVAL */
     int32_t reserved;     /* 0 */
     const void *q;        int64_t q_stride[3];
     const void *k;        int64_t k_stride[3];

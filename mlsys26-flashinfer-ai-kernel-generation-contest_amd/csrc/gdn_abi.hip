@@ -21,9 +21,15 @@ void gdn_begin_call() { g_last_error[0] = '\0'; }
 
 void gdn_begin_launches()
 {
-    // Drain an error an earlier HIP call left on this thread (a previous framework op),
-    // so that the checks after this call's launches report only its own.
-    (void)hipGetLastError();
+    // An error an earlier HIP call left pending on this thread (a previous framework op)
+    // is drained, so that the checks after this call's launches report only their own,
+    // and named in the last-error message, so that it is not lost: a call that then
+    // succeeds returns GDN_OK with that note in gdn_last_error().
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        gdn_set_error(GDN_OK, "note: a HIP error left pending by an earlier call was cleared "
+                      "before this call's launches: %s (%s)", hipGetErrorName(e),
+                      hipGetErrorString(e));
 }
 
 int gdn_check_launch(const char *what)

@@ -19,8 +19,8 @@
 // row is spread over 8 consecutive lanes and each lane owns 16 columns as four
 // float4 at columns 4s + 32j (s = lane % 8, j = 0..3), so one load instruction
 // of a wavefront covers eight full 128-byte row segments. Row sums are 8-lane
-// DPP reductions. Tuning variants change the workgroup size, lanes per row
-// (8 or 16) and rows per lane.
+// DPP reductions. The kernel template also takes other workgroup sizes, 16 lanes per
+// row and several rows per lane; only the shape above is instantiated.
 #include "gdn_common.h"
 
 #include <algorithm>
@@ -316,6 +316,8 @@ extern "C" int gdn_decode_launch(const gdn_decode_params *p, void *stream)
         return gdn_set_error(GDN_EINVAL, "gdn_decode: head_size %d unsupported (128 only)", D);
     if (T < 1)
         return gdn_set_error(GDN_EINVAL, "gdn_decode: seq_len %d must be >= 1", T);
+    if (p->variant != 0)
+        return gdn_set_error(GDN_EINVAL, "gdn_decode: variant %d unknown (0 only)", p->variant);
     if (B == 0)
         return GDN_OK;
     if (!p->q || !p->k || !p->v || !p->A_log || !p->a || !p->dt_bias || !p->b || !p->output ||
@@ -395,19 +397,7 @@ extern "C" int gdn_decode_launch(const gdn_decode_params *p, void *stream)
     a.g_is_h = ratio == 1;
     a.gmul = ratio == 1 ? 0u : (uint32_t)(((uint64_t(1) << 32) + ratio - 1) / ratio);
 
-    hipStream_t st = (hipStream_t)stream;
-    // variant (tuning sweeps): workgroup size x lanes per state row x rows per lane
-    // x non-temporal hint; 0 is the default.
-    switch (p->variant) {
-    case 1: return launch_cfg<256, 8, 2, true>(a, B, HQK, HV, st);
-    case 2: return launch_cfg<256, 8, 4, true>(a, B, HQK, HV, st);
-    case 3: return launch_cfg<256, 8, 1, false>(a, B, HQK, HV, st);
-    case 4: return launch_cfg<256, 16, 1, true>(a, B, HQK, HV, st);
-    case 5: return launch_cfg<128, 8, 1, true>(a, B, HQK, HV, st);
-    case 6: return launch_cfg<128, 16, 1, true>(a, B, HQK, HV, st);
-    case 7: return launch_cfg<256, 16, 2, true>(a, B, HQK, HV, st);
-    case 8: return launch_cfg<64, 8, 1, true>(a, B, HQK, HV, st);
-    default: return launch_cfg<256, 8, 1, true>(a, B, HQK, HV, st);
-    }
-
+    // 256 lanes, 8 lanes per state row, one row per lane, non-temporal state loads and
+    // stores: the fastest of the swept shapes at B = 1, 64 and 256 on MI355X
+    return launch_cfg<256, 8, 1, true>(a, B, HQK, HV, (hipStream_t)stream);
 }

@@ -451,12 +451,6 @@ struct ScanArgs {
     const int32_t *jobs;
     int job_first, njob_idx;
     float *seg_sin, *seg_r, *seg_mt;
-    // Fused kernel only (prep waves build each chunk's T', P' and gates in LDS): the gate
-    // inputs and the readout scale.
-    const bf16_t *a, *b;
-    const float *A_log, *dt_bias;
-    int64_t a_st, a_sh, b_st, b_sh, A_log_s, dt_s;
-    float scale;
 };
 
 
@@ -548,9 +542,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void
 gdn_prefill_prep2_kernel(PrepArgs p);
 template <bool SEG>
 __global__ __launch_bounds__(512) void gdn_prefill_scan8_kernel(ScanArgs p);
-// Whole sequences without a prep pass: 8 scan waves and 4 prep waves per workgroup; the prep
-// waves build chunk c + 1's T', P' and gates in LDS while the scan waves process chunk c.
-__global__ __launch_bounds__(768) void gdn_prefill_fused_kernel(ScanArgs p);
 template <bool SEG>
 __global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p);
 

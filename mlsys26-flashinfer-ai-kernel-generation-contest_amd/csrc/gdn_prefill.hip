@@ -135,6 +135,8 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
                              HQK, HV);
     if (D != 128)
         return gdn_set_error(GDN_EINVAL, "gdn_prefill: head_size %d unsupported (128 only)", D);
+    if (p->variant < 0 || p->variant > 2)
+        return gdn_set_error(GDN_EINVAL, "gdn_prefill: variant %d unknown (0, 1, 2)", p->variant);
     if (!p->q || !p->k || !p->v || !p->A_log || !p->a || !p->dt_bias || !p->b ||
         !p->cu_seqlens || !p->output || !p->new_state)
         return gdn_set_error(GDN_EINVAL, "gdn_prefill: NULL tensor pointer");
@@ -214,13 +216,8 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     const int G = p->variant == 0 ? L.G : 1;
     // Whole sequences: 4 scan waves per workgroup (two workgroups per (sequence, v-head))
     // when there are at most 128 (sequence, v-head) pairs, else 8 (129 to 256 pairs: the
-    // device picks, whole_dual below). Variants: 1 forces 4
-    // waves, 2 forces 8, 3 runs the fused kernel (8 scan waves and 4 prep waves, no prep
-    // pass and no records). The fused kernel is exact but slower on MI355X: the prep
-    // waves' per-chunk chain (copies, gates, P' and A, substitution, T chain, ~12k cycles)
-    // outlasts a scan chunk (~6.7k), so the scan waves wait for it at every chunk.
+    // device picks, whole_dual below). Variants: 1 forces 4 waves, 2 forces 8.
     const bool nw4 = p->variant == 1 || (p->variant == 0 && (int64_t)N * HV <= 128);
-    const bool fused = G == 1 && p->variant == 3;
     pa.seg_G = G;
     pa.seg_capA = (int)L.capA;
     // Pass C: the 4-wave kernel (two workgroups per (job, v-head), spread over twice the CUs)
@@ -232,7 +229,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
     pa.jobs = G > 1 ? (int32_t *)(ws + L.jobs) : nullptr;
     // Up to 64 sequences the prep kernel plans for itself (one dependent launch fewer:
     // the plan kernel's ~5 us sat on the critical path, mostly cu_seqlens load latency).
-    const bool prep_runs = L.nc > 0 && T > 0 && !fused;
+    const bool prep_runs = L.nc > 0 && T > 0;
     const bool self_plan = prep_runs && N >= 1 && N <= gdn::kSelfPlanMax;
     // Whole sequences, 129 to 256 (sequence, v-head) pairs: either scan can be the faster,
     // depending on the longest sequence, which only the device knows. Both are launched
@@ -334,17 +331,6 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
         sa.seg_sin = G > 1 ? (float *)(ws + L.seg_sin) : nullptr;
         sa.seg_r = G > 1 ? (float *)(ws + L.seg_r) : nullptr;
         sa.seg_mt = G > 1 ? (float *)(ws + L.seg_mt) : nullptr;
-        sa.a = (const gdn::bf16_t *)p->a;
-        sa.b = (const gdn::bf16_t *)p->b;
-        sa.A_log = p->A_log;
-        sa.dt_bias = p->dt_bias;
-        sa.a_st = p->a_stride[0];
-        sa.a_sh = p->a_stride[1];
-        sa.b_st = p->b_stride[0];
-        sa.b_sh = p->b_stride[1];
-        sa.A_log_s = p->A_log_stride;
-        sa.dt_s = p->dt_bias_stride;
-        sa.scale = p->scale;
         // 8 waves per workgroup = one (sequence, v-head) each, two waves per SIMD; with
         // few (sequence, v-head) pairs, 4 waves and two workgroups per pair spread the
         // state rows over twice as many CUs. variant: 1 forces 4 waves, 2 forces 8.
@@ -356,9 +342,7 @@ extern "C" int gdn_prefill_launch(const gdn_prefill_params *p, void *stream)
             if (ngroups > 0x7fffffff || blocks > 0x7fffffff)
                 return gdn_set_error(GDN_EINVAL, "gdn_prefill: grid too large");
             const dim3 grid((unsigned)blocks), b4(256), b8(512);
-            if (fused && !sa.jobs)
-                hipLaunchKernelGGL(gdn::gdn_prefill_fused_kernel, grid, dim3(768), 0, st, sa);
-            else if (sa.jobs && nw4)
+            if (sa.jobs && nw4)
                 hipLaunchKernelGGL(gdn::gdn_prefill_scan4_kernel<true>, grid, b4, 0, st, sa);
             else if (sa.jobs)
                 hipLaunchKernelGGL(gdn::gdn_prefill_scan8_kernel<true>, grid, b8, 0, st, sa);

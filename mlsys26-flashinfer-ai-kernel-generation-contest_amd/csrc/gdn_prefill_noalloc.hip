@@ -2,10 +2,11 @@
 // file-scope device array instead of a caller-provided buffer, for callers that cannot
 // allocate (code under HIP graph capture, tight serving loops, harnesses that forbid it).
 //
-// The array lives in this translation unit's own code object, so a process holds it on a
-// device only once it calls this entry point there (the runtime loads the code object and
-// its globals when the symbol is first resolved on that device), and then until the
-// process ends. Every call on one device shares that device's array: calls that overlap
+// The array lives in this translation unit's own code object. The runtime loads a code
+// object and allocates its globals on a device when one of its symbols is first used there
+// (deferred loading, the HIP runtime's default), so a process holds the array on a device
+// only once it calls this entry point there, and then until the process ends (measured on
+// MI355X: a decode-only process keeps the 96 MiB free; the first call takes them). Every call on one device shares that device's array: calls that overlap
 // in time on one device (different streams, or host threads without stream ordering)
 // race on it. Nothing in it needs to start at zero: the plan kernel writes every table
 // entry the later kernels read before they run.
@@ -25,11 +26,19 @@ void *g_scratch[kMaxDevices];  // device address of `scratch` on each device (nu
 
 // Device address of `scratch` on device dev, resolved once per device with that device
 // current. Host code never uses the array's name as an address: on the host it is a
-// stand-in symbol, not device memory.
-int scratch_ptr(int dev, void **out)
+// stand-in symbol, not device memory. Resolving it may load this code object and allocate
+// its globals, which a stream capture must not record: while `st` is being captured an
+// unresolved device is an error (the first call on a device comes before any capture).
+int scratch_ptr(int dev, hipStream_t st, void **out)
 {
     std::lock_guard<std::mutex> lock(g_mu);
     if (!g_scratch[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return gdn_set_error(GDN_EINVAL, "gdn_prefill_launch_noalloc: the first call on "
+                                 "device %d is inside a stream capture; make one call on "
+                                 "that device before capturing (it resolves the static "
+                                 "scratch)", dev);
         int cur = -1;
         if (hipGetDevice(&cur) != hipSuccess)
             return gdn_set_error(GDN_ELAUNCH, "gdn_prefill_launch_noalloc: hipGetDevice failed");
@@ -76,7 +85,7 @@ extern "C" int gdn_prefill_launch_noalloc(const gdn_prefill_params *p, void *str
     if (dev < 0 || dev >= kMaxDevices)
         return gdn_set_error(GDN_EINVAL, "gdn_prefill_launch_noalloc: device %d out of range", dev);
     void *ws = nullptr;
-    const int rc = scratch_ptr(dev, &ws);
+    const int rc = scratch_ptr(dev, st, &ws);
     if (rc)
         return rc;
     gdn_prefill_params q = *p;

@@ -1,7 +1,6 @@
 // Prefill scan kernels: the sequential chunk recurrence, state in registers, for whole
 // sequences or segment jobs.
 #include "gdn_prefill.h"
-#include "gdn_prefill_fused_prep.h"
 
 namespace gdn {
 
@@ -26,9 +25,6 @@ namespace gdn {
 // V columns are read with the LDS transpose read.
 // SEG: the grid walks segment jobs (p.jobs); otherwise whole sequences, and none of the
 // segment code is compiled in (it costs the whole-sequence loop registers).
-// FUSED (NW == 8, whole sequences): the workgroup has 4 more waves, the prep waves, which
-// build chunk c + 1's K, Q (copies), T', P' and gate area in the other chunk buffer while
-// the 8 scan waves process chunk c; the scan waves copy only V. No records are read.
 // A scan workgroup's job: its (sequence or segment job, q/k head) group grp, its place wi
 // among the group's workgroups, and the job's sequence, kind and chunk range.
 struct ScanJob {
@@ -95,11 +91,10 @@ __device__ __forceinline__ bool scan_job(const ScanArgs &p, ScanJob &j)
 // INST tags an instance: the whole-sequence body inside a segment kernel is instance 1, so
 // each instance is used by one kernel only (hipcc's host pass rejects a second kernel's use
 // of an instance of this device-only template: "substitution failure").
-template <int NW, bool SEG, bool FUSED = false, int INST = 0, int OUTS = -1>
+template <int NW, bool SEG, int INST = 0, int OUTS = -1>
 __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job, ScanBuf<NW> &BA,
-                                          ScanBuf<NW> &BB, FusedPrepScratch *ps = nullptr)
+                                          ScanBuf<NW> &BB)
 {
-    static_assert(!FUSED || (NW == 8 && !SEG), "the fused kernel scans whole sequences, 8 waves");
     constexpr int TPH = 8 / NW;  // workgroups per (sequence, v-head)
     const int grp = job.grp, wi = job.wi, n = job.n, tok0 = job.tok0, len = job.len,
               c0 = job.c0, kind = SEG ? job.kind : kJobFirst, cb = SEG ? job.cb : 0,
@@ -118,8 +113,6 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63,
               lr = l & 15, lg = l >> 4;
     const int v0w = v0 + 16 * w;
-    const bool prepw = FUSED && w >= NW;  // a prep wave (wave-uniform)
-    const int pw = w - NW;                // its column block
 
     // ---- copy plan. Every copy is a buffer load straight to LDS; per-lane source offsets
     // are chunk-invariant and computed once. Rows past a chunk's end fall outside the
@@ -138,33 +131,14 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
 
     constexpr int VWIN = 2 * NW;               // V windows
     constexpr int NWIN = 32 + VWIN + 19;       // all windows
-    // windows per wave (fused: scan waves copy 2 V windows, prep waves 8 K / Q windows)
-    constexpr int PER = FUSED ? 2 : (NWIN + NW - 1) / NW;
-    constexpr int PERP = 8;
+    constexpr int PER = (NWIN + NW - 1) / NW;  // windows per wave
 
     // Source offset of this lane in window i (compile-time) of this wave; window kinds
     // follow win = w + NW i: K rows 4b..4b+3 (16 windows), Q (16), V (NW == 8: 4 rows per
     // window, NW == 4: 8 rows), then 18 T' / P' windows and the gate area.
-    uint32_t woff[FUSED ? PERP : PER];
-    if constexpr (FUSED) {
-#pragma unroll
-        for (int i = 0; i < PERP; ++i) {
-            uint32_t off;
-            if (prepw) {  // K windows pw + 4 i, then Q windows pw + 4 (i - 4)
-                const int t = 4 * (pw + 4 * (i & 3)) + (l >> 4), cs = l & 15;
-                off = i < 4 ? (uint32_t)t * kst2 + 16u * (cs ^ kswz(t))
-                            : (uint32_t)t * qst2 + 16u * (cs ^ (t & 15));
-            } else {  // V windows w + 8 i
-                const int t = 4 * (w + NW * (i & 1)) + (l >> 4), cs = l & 15;
-                off = (uint32_t)t * vst2 + 16u * (cs ^ (2 * (t & 3)));
-            }
-            woff[i] = off;
-        }
-    }
+    uint32_t woff[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        if constexpr (FUSED)
-            break;
         const int win = w + NW * i;
         uint32_t off = 0;
         if (NW * i < 16) {
@@ -215,10 +189,6 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
     auto chunk_src = [&](int c) { return chunk_src_v(c, true); };
     auto issue_win = [&](ScanBuf<NW> &B, const ChunkSrc &cs, const int i) {
         const int win = w + NW * i;  // window kind is a compile-time function of i
-        if constexpr (FUSED) {  // scan waves: V windows w + 8 i
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.v, (GDN_LDS void *)&B.V[64 * win], 16, woff[i], 0, 0, 0);
-            return;
-        }
         if (NW * i < 16) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.k, (GDN_LDS void *)&B.K[64 * win], 16, woff[i], 0, 0, 0);
         } else if (NW * i < 32) {
@@ -248,19 +218,6 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
         for (int i = 0; i < PER; ++i)
             issue_win(B, cs, i);
     };
-    // prep waves: chunk c's K and Q into B
-    auto issue_kq = [&](ScanBuf<NW> &B, int c) {
-        const ChunkSrc cs = chunk_src(c);
-#pragma unroll
-        for (int i = 0; i < PERP; ++i) {
-            const int b = pw + 4 * (i & 3);
-            if (i < 4)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.k, (GDN_LDS void *)&B.K[64 * b], 16, woff[i], 0, 0, 0);
-            else
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(cs.q, (GDN_LDS void *)&B.Q[64 * b], 16, woff[i], 0, 0, 0);
-        }
-    };
-
     // ---- LDS read offsets (bytes within a ScanBuf member; chunk-invariant)
     const int c_ = lr & 3, r_ = lr >> 2;
     uint32_t koffA[4], ktoff[4], qoff[4];
@@ -303,47 +260,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
         for (int t = 0; t < 8; ++t)
             R[t] = *(const f32x4 *)(rp + 256 * t);
     };
-    // fused: the prep waves' meeting counter lives in the padding of buffer A's gate area
-    // (floats 193 .. 255 of it are never written or read otherwise)
-    int meet = 0;
-    int *const ctr = (int *)((float *)BA.G + 255);
-    auto prep_next = [&](ScanBuf<NW> &B, int c) {  // prep waves: chunk c into B
-        issue_kq(B, c);
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's K / Q copies landed
-        meet += kPrepWaves;
-        prep_meet(ctr, meet);                // ... and every prep wave's
-        if constexpr (FUSED)
-            fused_prep_chunk(p, B, *ps, ctr, meet, pw, h, (int64_t)tok0 + (int64_t)c * kC,
-                             min(kC, len - c * kC));
-    };
-    if constexpr (FUSED) {
-        // T' / P' of both buffers start at zero: the prep waves write only the blocks on
-        // and below the diagonal, and the scan reads some units above it as zeros
-        u32x4 *za = &BA.T[0][0], *zb = &BB.T[0][0];
-        static_assert(sizeof(BA.T) + sizeof(BA.P) == 1536 * 16, "T' and P' are adjacent");
-        for (int u = tid; u < 1536; u += 64 * (NW + kPrepWaves)) {
-            za[u] = u32x4{0u, 0u, 0u, 0u};
-            zb[u] = u32x4{0u, 0u, 0u, 0u};
-        }
-        if (tid == 0)
-            *ctr = 0;
-        lds_barrier();
-        if (prepw) {
-            // the prep waves' own loop, with the scan loop's barriers: one per chunk, after
-            // which chunk c is ready in its buffer (chunk c in BA when c - cb is even)
-            __builtin_amdgcn_s_setprio(3);  // their chain gates every chunk: first pick
-            if (ce > cb)
-                prep_next(BA, cb);
-            for (int c = cb; c < ce; ++c) {
-                dma_barrier();
-                if (c + 1 < ce)
-                    prep_next(((c + 1 - cb) & 1) ? BB : BA, c + 1);
-            }
-            return;
-        }
-        if (ce > cb)
-            issue_chunk(BA, cb);
-    } else if (chain) {
+    if (chain) {
         issue_m(q);
         load_r(q);
         // unconditional, so the number of operations in flight is the same on every path
@@ -673,7 +590,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
     // output stores, which nothing in the kernel reads, so it leaves them in flight
     // (waiting for them cost ~700 of a chunk's ~7000 cycles). Before the first chunk,
     // state loads the compiler may have ordered either way are in flight: wait for all.
-    const bool keep_stores = !FUSED && do_out;
+    const bool keep_stores = do_out;
     auto chunk_barrier = [&](bool first) {
         if (keep_stores && !first) {
             asm volatile("" ::: "memory");
@@ -776,13 +693,13 @@ __device__ __forceinline__ void scan_kernel_body(const ScanArgs &p, ScanBuf<NW> 
         return;
     if constexpr (SEG) {
         if (job.kind == kJobFirst && job.q < 0 && job.cb == 0) {
-            scan_body<NW, false, false, 1>(fresh_kernel_args(), job, BA, BB);
+            scan_body<NW, false, 1>(fresh_kernel_args(), job, BA, BB);
         } else if (job.kind == kJobFirst || job.kind == kJobResume) {
-            scan_body<NW, true, false, 0, 1>(fresh_kernel_args(), job, BA, BB);
+            scan_body<NW, true, 0, 1>(fresh_kernel_args(), job, BA, BB);
         } else if (job.kind == kJobZero) {
-            scan_body<NW, true, false, 0, 0>(fresh_kernel_args(), job, BA, BB);
+            scan_body<NW, true, 0, 0>(fresh_kernel_args(), job, BA, BB);
         } else {
-            scan_body<NW, true, false, 0, 2>(fresh_kernel_args(), job, BA, BB);
+            scan_body<NW, true, 0, 2>(fresh_kernel_args(), job, BA, BB);
         }
     } else {
         scan_body<NW, SEG>(p, job, BA, BB);
@@ -801,16 +718,6 @@ __global__ __launch_bounds__(256) void gdn_prefill_scan4_kernel(ScanArgs p)
 {
     __shared__ ScanBuf<4> bufA, bufB;
     scan_kernel_body<4, SEG>(p, bufA, bufB);
-}
-
-__global__ __launch_bounds__(768) void gdn_prefill_fused_kernel(ScanArgs p)
-{
-    __shared__ ScanBuf<8> bufA, bufB;
-    __shared__ FusedPrepScratch ps;
-    ScanJob job;
-    if (!scan_job<8, false>(p, job))
-        return;
-    scan_body<8, false, true>(p, job, bufA, bufB, &ps);
 }
 
 template __global__ void gdn_prefill_scan8_kernel<false>(ScanArgs p);

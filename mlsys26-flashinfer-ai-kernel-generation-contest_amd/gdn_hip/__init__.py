@@ -4,6 +4,6 @@
 entry points (``kernel.py::gdn_decode``, ``kernel.py::gdn_prefill``) and launch
 hand-written HIP kernels from libgdn_hip.so.
 """
-from .api import gdn_decode, gdn_prefill, release_workspace, set_decode_variant  # noqa: F401
+from .api import gdn_decode, gdn_prefill, graph_workspace_bytes, release_workspace  # noqa: F401
 
-__all__ = ["gdn_decode", "gdn_prefill", "release_workspace", "set_decode_variant"]
+__all__ = ["gdn_decode", "gdn_prefill", "graph_workspace_bytes", "release_workspace"]

@@ -169,7 +169,7 @@ def _decode_marshal(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_sta
     P.struct_size = ctypes.sizeof(_lib.DecodeParams)
     P.batch, P.seq_len, P.num_qk_heads, P.num_v_heads, P.head_size = B, T, HQK, HV, D
     P.scale = scale
-    P.variant = _decode_variant
+    P.variant = 0
     P.q, P.q_stride = _ptr(q_), _strides(q_, 4)
     P.k, P.k_stride = _ptr(k_), _strides(k_, 4)
     P.v, P.v_stride = _ptr(v_), _strides(v_, 4)
@@ -205,7 +205,7 @@ def gdn_decode(q, k, v, state, A_log, a, dt_bias, b, scale, output=None, new_sta
         fast = _lib.fast()
         if fast is not None and fast.decode(q, k, v, state, A_log, a, dt_bias, b,
                                             0.0 if scale is None else scale, output,
-                                            new_state, _decode_variant) == 0:
+                                            new_state, 0) == 0:
             return output, new_state
     with torch.no_grad():
         P, output, new_state, copy_back, _keep = _decode_marshal(
@@ -246,21 +246,13 @@ class DecodePlan:
         return self.output, self.new_state
 
 
-_decode_variant = 0
-
-
-def set_decode_variant(v: int) -> None:
-    """Select a decode kernel variant (tuning sweeps; 0 = tuned default)."""
-    global _decode_variant
-    _decode_variant = int(v)
-
-
 # ----------------------------------------------------------------------------- prefill
 _prefill_variant = 0
 
 
 def set_prefill_variant(v: int) -> None:
-    """Select a prefill kernel variant (tuning sweeps; 0 = tuned default)."""
+    """Select a prefill kernel variant: 0 = tuned default; 1 / 2 scan every sequence whole
+    with 4 / 8 scan waves per workgroup (no segments)."""
     global _prefill_variant
     _prefill_variant = int(v)
 
@@ -275,9 +267,12 @@ def _workspace(dev, stream, nbytes):
 
     Eager calls share a grow-only buffer per (device, stream), rewritten by every call
     (stream order keeps calls on one stream apart). A call being captured into a HIP
-    graph gets a buffer of its own that is never freed or reused: the graph's kernels
-    keep pointing at it for as long as the graph may be replayed, and graphs captured
-    on the shared capture stream must not share (or free) one another's workspace."""
+    graph gets a buffer of its own, kept until ``release_workspace(graphs=True)``: the
+    graph's kernels keep pointing at it for as long as the graph may be replayed, and
+    graphs captured on the shared capture stream must not share (or free) one another's
+    workspace. Each capture adds one (about 72 MB at 8K tokens in 16 sequences), so a
+    caller that captures many graphs releases them once it has destroyed those graphs,
+    or uses gdn_prefill_launch_noalloc, whose workspace is one static array."""
     if torch.cuda.is_current_stream_capturing():
         buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
         with _ws_lock:
@@ -292,12 +287,22 @@ def _workspace(dev, stream, nbytes):
         return buf
 
 
-def release_workspace() -> None:
+def graph_workspace_bytes() -> int:
+    """Bytes held by the workspaces of captured prefills (see ``release_workspace``)."""
+    with _ws_lock:
+        return sum(b.numel() for b in _graph_ws)
+
+
+def release_workspace(graphs: bool = False) -> None:
     """Drop the cached eager prefill workspaces, the Python path's and the fast path's
     (they return to torch's caching allocator; the caller synchronises first, so that no
-    call in flight still uses them). Workspaces of captured graphs are kept."""
+    call in flight still uses them). With ``graphs=True`` also drop the workspaces of every
+    prefill captured into a HIP graph so far: only once every graph that holds such a
+    prefill has been destroyed (replaying one afterwards reads freed memory)."""
     with _ws_lock:
         _ws_cache.clear()
+        if graphs:
+            _graph_ws.clear()
     fast = _lib.fast()
     if fast is not None:
         fast.release_workspace()

@@ -2,9 +2,12 @@
 
 A flashinfer-bench style harness imports this file and calls ``gdn_decode`` with the
 definition's inputs positionally, then the preallocated outputs (README.md:227-257).
-The arithmetic runs in libgdn_hip.so, which the solution's build step makes
-(``python -m gdn_hip.build`` in the unpacked solution); importing raises if it is
-missing, so no compile ever lands inside a timed process.
+The arithmetic runs in libgdn_hip.so. A packed solution carries sources only
+(gdn_decode/scripts/pack_solution.py:34-82), so the first import builds the library
+(hipcc for gfx950, about 10 s) and the C++ fast path of the entry points (about 40 s;
+without it calls take the slower Python validation path) next to the sources, as
+FAQ.md:138 asks of a solution with its own kernels: the compile lands in the harness's
+import phase, never in a timed call. Later imports load what is built.
 """
 import os
 import sys
@@ -16,7 +19,10 @@ _ROOT = next((r for r in (_HERE, os.path.dirname(os.path.dirname(_HERE)))
 if _ROOT not in sys.path:
     sys.path.insert(0, _ROOT)
 
+from gdn_hip import build as _build  # noqa: E402
+
+_build.ensure_built()
 from gdn_hip import _lib  # noqa: E402
 from gdn_hip.api import gdn_decode  # noqa: E402,F401
 
-_lib.load()  # RuntimeError if libgdn_hip.so is not built: run python -m gdn_hip.build
+_lib.load()

@@ -94,6 +94,19 @@ def test_decode_rejects_bad_params_without_launch():
     assert "NULL" in _lib.last_error()
     P.batch = 0  # empty batch is a no-op success
     assert lib.gdn_decode_launch(ctypes.byref(P), None) == _lib.GDN_OK
+    P.variant = 3  # only the tuned kernel is built
+    assert lib.gdn_decode_launch(ctypes.byref(P), None) == _lib.GDN_EINVAL
+    assert "variant" in _lib.last_error()
+
+
+def test_prefill_rejects_unknown_variant_without_launch():
+    lib = _lib.load()
+    P = _lib.PrefillParams()
+    P.struct_size = ctypes.sizeof(_lib.PrefillParams)
+    P.total_tokens, P.num_seqs, P.num_qk_heads, P.num_v_heads, P.head_size = 64, 1, 16, 32, 128
+    P.variant = 3
+    assert lib.gdn_prefill_launch(ctypes.byref(P), None) == _lib.GDN_EINVAL
+    assert "variant" in _lib.last_error()
 
 
 def test_decode_rejects_bad_layout_without_launch():

@@ -78,6 +78,35 @@ def test_prefill_empty_sequences_and_gaps(dev):
          "empty+gaps")
 
 
+@pytest.mark.parametrize("scale", [None, 0.0, 0.25, "host tensor", "device tensor"])
+def test_prefill_scale_defaults(dev, scale):
+    """scale None / 0 -> 1/sqrt(D) (gdn_prefill/solution/triton/kernel.py:276-277); a
+    one-element tensor is read as its value (0.25 here). Through the Python path (no
+    destination buffers), destination-passing calls (the C++ fast path for a float or None
+    scale, the Python path for a tensor) and the fast path called directly, each against
+    the oracle."""
+    inp = prefill_inputs([150, 64, 1], hqk=4, hv=8, seed=31, with_state=True)
+    inp.scale = 0.25 if isinstance(scale, str) else scale
+    ref_o, ref_s = _oracle(inp)
+    g = inp.to(dev)
+    args = list(g.args())
+    if isinstance(scale, str):
+        args[-1] = torch.tensor([0.25], device=dev if scale == "device tensor" else "cpu")
+    T, N = g.q.shape[0], len(inp.seqlens)
+    out, ns = gdn_prefill(*args)
+    o2 = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=dev)
+    n2 = torch.empty((N, 8, 128, 128), dtype=torch.float32, device=dev)
+    gdn_prefill(*args, output=o2, new_state=n2)
+    torch.cuda.synchronize()
+    _check(out, ns, ref_o, ref_s, f"scale={scale}")
+    _check(o2, n2, ref_o, ref_s, f"scale={scale} destination-passing")
+    if not isinstance(scale, str):
+        o3, n3 = torch.empty_like(o2), torch.empty_like(n2)
+        assert _lib.fast().prefill(*args[:-1], 0.0 if scale is None else scale, o3, n3, 0) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(o3, out) and torch.equal(n3, ns)
+
+
 def test_prefill_int64_cu_seqlens(dev):
     _run(dev, prefill_inputs([99, 1, 250], seed=19, with_state=True, cu_dtype=torch.int64),
          "cu int64")
@@ -625,25 +654,3 @@ def test_prefill_fast_path_declines_capture_and_odd_layouts(dev):
     with torch.cuda.graph(graph):
         rc = fast.prefill(*g.args(), out, ns, 0)
     assert rc == 1
-
-
-@pytest.mark.parametrize("lens,hqk,hv,gates", [(None, 16, 32, "strong"), ([700, 5, 64, 129], 4, 8, "mild")])
-def test_prefill_fused_kernel_variant(dev, lens, hqk, hv, gates):
-    """The fused kernel (prep waves building each chunk's T', P' and gates in LDS beside the
-    scan waves; variant 3) matches the oracle and the default path bit for bit."""
-    from gdn_hip.api import set_prefill_variant
-
-    lens = lens or varlen_lengths(16, seed=5)
-    inp = prefill_inputs(lens, hqk=hqk, hv=hv, seed=55, with_state=True, gates=gates)
-    ref_o, ref_s = _oracle(inp)
-    g = inp.to(dev)
-    try:
-        set_prefill_variant(3)
-        o3, s3 = gdn_prefill(*g.args())
-        set_prefill_variant(2)
-        o2, s2 = gdn_prefill(*g.args())
-    finally:
-        set_prefill_variant(0)
-    torch.cuda.synchronize()
-    _check(o3, s3, ref_o, ref_s, f"fused hqk={hqk} hv={hv} {gates}")
-    assert torch.equal(o3, o2) and torch.equal(s3, s2)

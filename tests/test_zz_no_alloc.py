@@ -1,8 +1,14 @@
 """gdn_prefill_launch_noalloc (static device scratch, no allocation) against
 gdn_prefill_launch (caller-owned workspace), both called through the C ABI on the same
 inputs: bit-identical outputs and states on two calls in a row, the second smaller than
-the first, and a clear rejection of a size beyond the static scratch."""
+the first, and a clear rejection of a size beyond the static scratch. Under HIP graph
+capture: replays match the eager call, and (in a fresh child process) a first call inside
+a capture is refused cleanly; the same child measures when the scratch is taken."""
 import ctypes
+import json
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -67,3 +73,52 @@ def test_noalloc_rejects_oversize(dev):
     rc = lib.gdn_prefill_launch_noalloc(ctypes.byref(P), None)
     assert rc == _lib.GDN_EWORKSPACE
     assert "static scratch" in _lib.last_error()
+
+
+def test_noalloc_in_graph_after_eager_call(dev):
+    """After an eager call on the device, a noalloc prefill captured into a HIP graph
+    replays bit-identically to the eager result (three replays, eager noalloc calls on
+    other inputs between them)."""
+    lib = _lib.load()
+    inp, eo, en = _both(dev, [700, 64, 1], 21, True)  # eager noalloc call first
+    g = inp.to(dev)
+    out, ns = torch.full_like(eo, 3.0), torch.full_like(en, 3.0)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        P, _, _, copy_back, keep, stream = _prefill_marshal(*g.args(), out, ns,
+                                                            with_workspace=False)
+        rc = lib.gdn_prefill_launch_noalloc(ctypes.byref(P), ctypes.c_void_p(stream.cuda_stream))
+    assert rc == _lib.GDN_OK, _lib.last_error()
+    for r in range(3):
+        out.fill_(3.0)
+        ns.fill_(3.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"[noalloc graph] replay {r}: {torch.equal(out, eo)} {torch.equal(ns, en)}",
+              flush=True)
+        assert torch.equal(out, eo) and torch.equal(ns, en), f"replay {r} differs"
+        _both(dev, [90, 200], 30 + r, False)  # other calls overwrite the scratch
+
+
+def test_noalloc_fresh_process_capture_and_memory():
+    """In a child process with no earlier noalloc call: a first call inside a capture
+    returns GDN_EINVAL with a clear message and takes no memory; the first eager call
+    takes the 96 MiB scratch (a decode and a workspace prefill before it did not); a
+    capture after it replays bit-identically."""
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_fresh_process.py")
+    print("[noalloc fresh process] starting child", flush=True)
+    res = subprocess.run([sys.executable, script], capture_output=True, text=True, timeout=240)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    cap = 96 << 20
+    assert r["first_in_capture_rc"] == _lib.GDN_EINVAL
+    assert "before capturing" in r["first_in_capture_msg"]
+    assert r["free_before"] - r["free_after_refused"] < cap // 2
+    taken = r["free_before"] - r["free_after_first_call"]
+    print(f"[noalloc fresh process] first call took {taken / 2**20:.1f} MiB", flush=True)
+    assert cap <= taken < cap + (16 << 20)
+    assert r["eager_rc"] == 0 and r["capture_rc"] == 0
+    assert r["replays_bitwise"] == [True, True, True]
+
