@@ -95,8 +95,13 @@ def bench_decode(steps, warmup, batch=64, nsets=4, inplace=False):
     return dict(ms=ms, gbs=gbs, bytes=nbytes, trials=trials)
 
 
-def bench_prefill(steps, warmup, lens=None, with_state=True):
-    """Prefill over `lens` (default: 16 sequences, lengths ~U[64,1024] from seed 0)."""
+def bench_prefill(steps, warmup, lens=None, with_state=True, settle_ms=0.0):
+    """Prefill over `lens` (default: 16 sequences, lengths ~U[64,1024] from seed 0).
+
+    `warmup` calls, then back-to-back calls for at least `settle_ms` of GPU time before the
+    timed trials: under this sustained MFMA and HBM load the clock management runs the first
+    ~100-200 calls slower (up to ~25 % at 8172 tokens) before it settles
+    (profiles/prefill_clock_curve.md), and a serving loop runs in the settled state."""
     import torch
 
     from gdn_hip import gdn_prefill
@@ -112,6 +117,15 @@ def bench_prefill(steps, warmup, lens=None, with_state=True):
         gdn_prefill(*inp.args(), output=out, new_state=ns)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
+    settled = 0.0
+    while settled < settle_ms:
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(20):
+            gdn_prefill(*inp.args(), output=out, new_state=ns)
+        s1.record(stream)
+        torch.cuda.synchronize()
+        settled += s0.elapsed_time(s1)
     trials = []
     for _ in range(3):
         start = torch.cuda.Event(enable_timing=True)
@@ -127,7 +141,36 @@ def bench_prefill(steps, warmup, lens=None, with_state=True):
     flops = prefill_flops(T)
     tflops = flops / (ms * 1e-3) / 1e12
     return dict(tokens=T, nseqs=len(lens), ms=ms, mtok_s=T / (ms * 1e-3) / 1e6, tflops=tflops,
-                mfma_frac=tflops / BF16_PEAK_TFLOPS)
+                mfma_frac=tflops / BF16_PEAK_TFLOPS, settle_ms=round(settled, 1), trials=trials)
+
+
+def prefill_curve(batches, lens=None, with_state=True):
+    """us/call of back-to-back prefills, per batch of 20 calls, from the process's first
+    call on: how the clock management settles under this load."""
+    import torch
+
+    from gdn_hip import gdn_prefill
+    from gdn_hip.inputs import prefill_inputs, varlen_lengths
+
+    dev = torch.device("cuda", 0)
+    lens = lens or varlen_lengths(16, seed=0)
+    inp = prefill_inputs(lens, seed=0, with_state=with_state).to(dev)
+    T = sum(lens)
+    out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((len(lens), 32, 128, 128), dtype=torch.float32, device=dev)
+    gdn_prefill(*inp.args(), output=out, new_state=ns)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(batches + 1)]
+    ev[0].record(stream)
+    for b in range(batches):
+        for _ in range(20):
+            gdn_prefill(*inp.args(), output=out, new_state=ns)
+        ev[b + 1].record(stream)
+    torch.cuda.synchronize()
+    us = [ev[i].elapsed_time(ev[i + 1]) / 20 * 1e3 for i in range(batches)]
+    print(json.dumps({"workload": f"prefill T={T} ({len(lens)} sequences)",
+                      "us_per_call_per_batch_of_20": [round(x, 1) for x in us]}), flush=True)
 
 
 def _host_cores():
@@ -186,25 +229,87 @@ def cpu_baseline_prefill(budget_s=5.0):
                        f"{sec * 1e3:.1f} ms/step")
 
 
-def summarize_trace(path, skip_first=0):
+def summarize_trace(path, skip_first=0, last=0):
     """Per-kernel dispatch durations from a rocprofv3 kernel_trace.csv, dropping each
-    kernel's first `skip_first` dispatches (the warmup calls); prints a markdown table."""
+    kernel's first `skip_first` dispatches (the warmup calls), or keeping only its `last`
+    ones (the timed calls after the prefill's settling phase); prints a markdown table."""
     import csv
     from collections import defaultdict
 
     per = defaultdict(list)
     with open(path) as f:
         for row in csv.DictReader(f):
-            per[row["Kernel_Name"]].append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
-    print(f"| kernel | dispatches (after skipping {skip_first}) | avg us | min us | max us |")
+            per[row["Kernel_Name"]].append((int(row["Start_Timestamp"]),
+                                            int(row["End_Timestamp"]) - int(row["Start_Timestamp"])))
+    per = {k: [d for _, d in sorted(v)] for k, v in per.items()}
+    sel = (lambda d: d[-last:]) if last > 0 else (lambda d: d[skip_first:])
+    what = f"the last {last}" if last > 0 else f"after skipping {skip_first}"
+    print(f"| kernel | dispatches ({what}) | avg us | min us | max us |")
     print("|---|---|---|---|---|")
-    for name, d in sorted(per.items(), key=lambda kv: -sum(kv[1][skip_first:])):
-        d = d[skip_first:]
+    for name, d in sorted(per.items(), key=lambda kv: -sum(sel(kv[1]))):
+        d = sel(d)
         if not d:
             continue
         short = name.split("(")[0][:90]
         print(f"| `{short}` | {len(d)} | {sum(d) / len(d) / 1e3:.2f} | {min(d) / 1e3:.2f} | "
               f"{max(d) / 1e3:.2f} |")
+
+
+def summarize_pmc(fetch_csv, write_csv, skip_first=0, algo_bytes=None, title=""):
+    """HBM traffic per kernel from two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE;
+    counter_collection.csv of each), scaled by what the same counters read for the
+    268,435,456-byte device copy of --calibrate-copy in those runs; prints the summary
+    that profiles/*_traffic.txt hold, ending in a traffic_bytes_per_launch line."""
+    import csv
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(list))
+    for path in (fetch_csv, write_csv):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                vals[row["Kernel_Name"]][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    # calibration kernel: torch's elementwise multiply of --calibrate-copy (its own kernel:
+    # reads 256 MiB, writes 256 MiB); the runtime's copy kernel is listed beside it
+    ref = next((k for k in vals if "elementwise" in k and "MulFunctor" in k), None)
+    if ref is None:
+        ref = next((k for k in vals if "elementwise" in k), None)
+    if ref is None:
+        raise SystemExit("no calibration kernel in the counter files: run with --calibrate-copy")
+    copy_bytes = 268435456
+    avg = lambda k, c: sum(vals[k][c]) / len(vals[k][c])  # noqa: E731
+    fk, wk = avg(ref, "FETCH_SIZE"), avg(ref, "WRITE_SIZE")
+    rf, wf = copy_bytes / (fk * 1024), copy_bytes / (wk * 1024)
+    print(f"# {title}".rstrip())
+    print(f"# Calibration: an elementwise multiply over {copy_bytes:,} bytes reads FETCH_SIZE = "
+          f"{fk:,.1f} KiB and writes WRITE_SIZE = {wk:,.1f} KiB")
+    print(f"#   => read factor {rf:.3f}, write factor {wf:.3f} (bytes per counted KiB / 1024)")
+    for k in vals:
+        if "copyBuffer" in k:
+            print(f"#   (the runtime's copy kernel of the same size reads FETCH_SIZE = "
+                  f"{avg(k, 'FETCH_SIZE'):,.1f} KiB, writes WRITE_SIZE = {avg(k, 'WRITE_SIZE'):,.1f} KiB)")
+    print(f"# averages per dispatch over the timed calls (first {skip_first} dispatches of each "
+          "kernel dropped)")
+    print("#")
+    print(f"# {'kernel':40s} {'dispatches':>10s} {'FETCH KiB':>12s} {'bytes read':>14s} "
+          f"{'WRITE KiB':>12s} {'bytes written':>14s}")
+    total = 0.0
+    for name, c in sorted(vals.items()):
+        if name == ref or "fillBuffer" in name or "copyBuffer" in name or "elementwise" in name:
+            continue
+        fv, wv = c.get("FETCH_SIZE", [])[skip_first:], c.get("WRITE_SIZE", [])[skip_first:]
+        if not fv or not wv:
+            continue
+        f_avg, w_avg = sum(fv) / len(fv), sum(wv) / len(wv)
+        rb, wb = f_avg * 1024 * rf, w_avg * 1024 * wf
+        total += rb + wb
+        short = name.split("(")[0].replace("void ", "")[:40]
+        print(f"# {short:40s} {len(fv):10d} {f_avg:12,.1f} {rb:14,.0f} {w_avg:12,.1f} {wb:14,.0f}")
+    print("#")
+    print(f"# measured total per launch (all kernels above) = {total:,.0f} B")
+    if algo_bytes:
+        print(f"# algorithmic bytes = {algo_bytes:,} -> measured / algorithmic = "
+              f"{total / algo_bytes:.2f}")
+    print(f"traffic_bytes_per_launch: {int(total)}")
 
 
 def main():
@@ -217,6 +322,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU work for the decode B=64 baseline (B=1 takes "
                          "0.15 of it, the prefill 0.6)")
+    ap.add_argument("--prefill-settle-ms", type=float, default=40.0,
+                    help="prefill lines: back-to-back calls for this much GPU time after the "
+                         "warmup calls, before timing (clock settling under sustained load)")
     ap.add_argument("--only", choices=["all", "decode", "prefill", "prefill4k"], default="all",
                     help="run one path only (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -224,10 +332,25 @@ def main():
     ap.add_argument("--trace-summary", metavar="CSV",
                     help="summarise a rocprofv3 kernel_trace.csv per kernel and exit")
     ap.add_argument("--skip-first", type=int, default=0,
-                    help="with --trace-summary: dispatches to drop per kernel (warmup)")
+                    help="with --trace-summary / --pmc-summary: dispatches to drop per kernel")
+    ap.add_argument("--curve", type=int, default=0, metavar="BATCHES",
+                    help="print the prefill's us/call over BATCHES back-to-back batches of 20 "
+                         "calls from a cold start (--only prefill or prefill4k), and exit")
+    ap.add_argument("--last", type=int, default=0,
+                    help="with --trace-summary: keep only each kernel's last N dispatches")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) per "
+                         "kernel with the copy calibration, and exit")
+    ap.add_argument("--algo-bytes", type=int, default=None,
+                    help="with --pmc-summary: algorithmic bytes per launch to compare against")
+    ap.add_argument("--title", default="", help="with --pmc-summary: heading line")
     args = ap.parse_args()
     if args.trace_summary:
-        summarize_trace(args.trace_summary, args.skip_first)
+        summarize_trace(args.trace_summary, args.skip_first, args.last)
+        return
+    if args.pmc_summary:
+        summarize_pmc(*args.pmc_summary, skip_first=args.skip_first,
+                      algo_bytes=args.algo_bytes, title=args.title)
         return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this path runs on one GPU "
@@ -248,14 +371,20 @@ def main():
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
+            torch.mul(src, 2.0, out=dst)  # an elementwise kernel: reads and writes 256 MiB
         torch.cuda.synchronize()
-        log("copy calibration: 3 x 268435456-byte device copies")
+        log("copy calibration: 3 x 268435456-byte device copies and elementwise multiplies")
         del src, dst
     psteps = max(3, min(args.steps, 50))
     pwarm = 5
+    if args.curve:
+        lens, st = (None, True) if args.only != "prefill4k" else ([4096], False)
+        prefill_curve(args.curve, lens=lens, with_state=st)
+        return
     if args.only in ("prefill", "prefill4k"):
         lens, st = (None, True) if args.only == "prefill" else ([4096], False)
-        pre = bench_prefill(psteps, pwarm, lens=lens, with_state=st)
+        pre = bench_prefill(psteps, pwarm, lens=lens, with_state=st,
+                            settle_ms=args.prefill_settle_ms)
         log(f"prefill: T={pre['tokens']} {pre['ms'] * 1e3:.1f} us/step "
             f"{pre['mtok_s']:.1f} Mtok/s {pre['tflops']:.1f} TFLOP/s")
         return
@@ -272,10 +401,11 @@ def main():
     pre = pre4k = None
     if not args.no_prefill:
         log(f"prefill 16x varlen: warmup {pwarm}, steps {psteps}")
-        pre = bench_prefill(psteps, pwarm)
+        pre = bench_prefill(psteps, pwarm, settle_ms=args.prefill_settle_ms)
         log(f"prefill: T={pre['tokens']} {pre['ms'] * 1e3:.1f} us/step "
             f"{pre['mtok_s']:.1f} Mtok/s {pre['tflops']:.1f} TFLOP/s")
-        pre4k = bench_prefill(psteps, pwarm, lens=[4096], with_state=False)
+        pre4k = bench_prefill(psteps, pwarm, lens=[4096], with_state=False,
+                              settle_ms=args.prefill_settle_ms)
         log(f"prefill 1x4096: {pre4k['ms'] * 1e3:.1f} us/step {pre4k['tflops']:.1f} TFLOP/s")
     cpu = cpu_more = None
     if not args.no_cpu:
@@ -331,22 +461,29 @@ def main():
         },
     }
     if pre is not None:
-        for key, r, wl, st in (("prefill_single_4k", pre4k, "GDN prefill, 1 sequence x 4096 "
-                                "tokens, zero initial state", False),
-                               ("prefill", pre, f"GDN prefill, {pre['nseqs']} sequences, lengths "
-                                f"~U[64,1024] (seed 0), T={pre['tokens']} tokens, non-zero fp32 "
-                                "initial state", True)):
-            hbm = prefill_bytes(r["tokens"], r["nseqs"], with_state=st) / (r["ms"] * 1e-3) / 1e9
+        for key, r, wl, st, tfile in (
+                ("prefill_single_4k", pre4k, "GDN prefill, 1 sequence x 4096 tokens, zero "
+                 "initial state", False, "prefill_4k_traffic.txt"),
+                ("prefill", pre, f"GDN prefill, {pre['nseqs']} sequences, lengths ~U[64,1024] "
+                 f"(seed 0), T={pre['tokens']} tokens, non-zero fp32 initial state", True,
+                 "prefill_varlen16_traffic.txt")):
+            algo = prefill_bytes(r["tokens"], r["nseqs"], with_state=st)
+            hbm = algo / (r["ms"] * 1e-3) / 1e9
             rec[key] = {
                 "workload": wl,
                 "us_per_step": round(r["ms"] * 1e3, 2),
                 "mtok_per_s": round(r["mtok_s"], 2),
                 "tflops": round(r["tflops"], 2),
+                # traffic: measured HBM bytes of all kernels of one prefill (FETCH_SIZE +
+                # WRITE_SIZE, copy-calibrated) against `algo_bytes`
                 "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
                              "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                             "frac": round(r["mfma_frac"], 4)},
+                             "frac": round(r["mfma_frac"], 4),
+                             "traffic": _traffic_from_profile(tfile), "algo_bytes": algo},
                 "hbm_gb_per_s": round(hbm, 1),
                 "hbm_frac": round(hbm / HBM_PEAK_GBS, 4),
+                "warmup_calls": pwarm,
+                "settle_ms": r["settle_ms"],
             }
     print(json.dumps(rec), flush=True)
 
