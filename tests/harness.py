@@ -20,6 +20,7 @@ the reference's drivers and their external harness do for this path:
   (computer_track_scores_local.py:157-158).
 
     python tests/harness.py [--out harness.json] [--quick] [--filter SUBSTR]
+    python tests/harness.py --render-md harness.json
 """
 from __future__ import annotations
 
@@ -144,13 +145,57 @@ def kernel_scores(results):
     return scores
 
 
+def render_md(doc, json_name):
+    """Markdown rendering of a results document (the table of profiles/harness_workloads.md)."""
+    lines = [
+        "# Per-workload records of tests/harness.py (flashinfer-bench record fields)", "",
+        "MI355X, one GPU. Commands (from the repository root): `python tests/harness.py --out "
+        f"gpurun_out/harness.json`, then `python tests/harness.py --render-md "
+        f"gpurun_out/harness.json`. The JSON document is committed beside this file as "
+        f"`{json_name}`, in the reference's results-file layout "
+        "(gdn_decode/results/*.json: solution_name, definition(s), timestamp, gpu, "
+        "benchmark_config, results per definition and workload).", "",
+        "Decode: warmup 3 / 100 iterations / 5 trials; prefill: 1 / 10 / 3 "
+        "(gdn_decode/scripts/run_local.py:33, gdn_prefill/scripts/run_local.py:33), median "
+        "trial, HIP events on the launch stream. `latency` is the public entry point called "
+        "destination-passing style, host cost included; `prevalidated` is the same launch "
+        "through a pre-marshalled `DecodePlan`. `reference` is the float64 CPU oracle on the "
+        "host. Status: output within atol = rtol = 1e-2 and new_state within rtol 1e-3 / atol "
+        "1e-4 elementwise and 1e-3 normwise.", "",
+        "Like flashinfer-bench, every iteration of a workload reuses one set of buffers, so "
+        "working sets below the 256 MB Infinity Cache (e.g. qk4_v8 decode at B=64: 64 MiB) stay "
+        "resident between iterations: these latencies are not HBM figures (bench.py rotates "
+        "buffer sets for that).", "",
+        f"GPU: {doc['gpu']}; timestamp {doc['timestamp']}.", "",
+        "| definition | workload | status | latency us | prevalidated us | reference ms | "
+        "speedup | output max abs err | state norm rel err |",
+        "|---|---|---|---|---|---|---|---|---|"]
+    for defn, ents in doc["results"].items():
+        for name, e in ents.items():
+            pv = e.get("prevalidated_latency_ms")
+            pvs = "" if pv is None else f"{pv * 1e3:.2f}"
+            lines.append(f"| {defn} | {name} | {e['status']} | {e['latency_ms'] * 1e3:.2f} | "
+                         f"{pvs} | {e['reference_latency_ms']:.2f} | {e['speedup_factor']:.0f} | "
+                         f"{e['output_max_abs_error']:.1e} | {e['state_norm_rel_error']:.1e} |")
+    lines += ["", "Kernel scores (mean speedup per definition, zeroed by any failed workload, "
+              "computer_track_scores_local.py:157-158): "
+              + ", ".join(f"{k} {v:.0f}" for k, v in doc["kernel_scores"].items())]
+    return "\n".join(lines) + "\n"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=None)
+    ap.add_argument("--render-md", metavar="RESULTS_JSON", default=None,
+                    help="print the markdown table of a results document and exit")
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--filter", default="",
                     help="run only workloads whose '<definition>/<workload>' contains this")
     args = ap.parse_args()
+    if args.render_md:
+        with open(args.render_md) as f:
+            sys.stdout.write(render_md(json.load(f), "harness_workloads.json"))
+        return
     if not torch.cuda.is_available():
         print("harness: no HIP device", file=sys.stderr)
         sys.exit(1)
