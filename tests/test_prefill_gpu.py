@@ -594,6 +594,38 @@ def test_prefill_graphs_keep_their_own_workspaces(dev):
         assert torch.equal(o, eo) and torch.equal(n, en), f"replay {r} differs"
 
 
+def test_prefill_graph_workspaces_released_with_the_graphs(dev):
+    """A captured prefill holds a workspace of its own until the caller, having destroyed the
+    graph, calls release_workspace(graphs=True); the graph's replay before that matches its
+    eager result, and a new capture after the release works again."""
+    from gdn_hip import graph_workspace_bytes
+
+    g = prefill_inputs([300, 41], seed=77, with_state=True).to(dev)
+    T, N = g.q.shape[0], 2
+    out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((N, 32, 128, 128), dtype=torch.float32, device=dev)
+    gdn_prefill(*g.args(), output=out, new_state=ns)
+    torch.cuda.synchronize()
+    eo, en = out.clone(), ns.clone()
+    need = _lib.load().gdn_prefill_workspace_size(T, N, 16, 32, 128)
+    for rnd in range(2):
+        before = graph_workspace_bytes()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            gdn_prefill(*g.args(), output=out, new_state=ns)
+        assert graph_workspace_bytes() - before >= need
+        out.zero_()
+        ns.zero_()
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eo) and torch.equal(ns, en), f"round {rnd}: replay differs"
+        del gr
+        torch.cuda.synchronize()
+        release_workspace(graphs=True)
+        assert graph_workspace_bytes() == 0
+
+
 def test_prefill_fast_path_taken_and_exact(dev):
     """A destination-passing prefill outside capture goes through the C++ fast path: it
     launches (returns 0), matches the oracle and equals the Python path bit for bit; after
