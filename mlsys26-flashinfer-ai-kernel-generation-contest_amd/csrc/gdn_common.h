@@ -43,6 +43,32 @@ __device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t &hi, uin
     lo = pack_bf16x2(a - bf16lo(hi), b - bf16hi(hi));
 }
 
+// The same split with each residual x - bf16(x) formed by one dot product,
+// v_dot2c_f32_bf16: hi . {-1, 0} + a and hi . {0, -1} + b (exact: the residual is an fp32
+// value). The instruction accumulates into its destination, so the split writes a and b's
+// registers when they die there. The two multipliers are kept in SGPRs, made once per kernel
+// by split_consts(): left as immediates, the compiler encodes {-1, 0} as the inline
+// constant -1.0, which the hardware reads as the fp32 pattern 0xbf800000, i.e. {0, -1}
+// (checked on MI355X over 2^20 inputs: every residual of the SGPR form matches a - bf16(a)
+// bit for bit; the immediate form gets almost all of them wrong).
+struct SplitConsts {
+    bf16x2_t m0, m1;
+};
+__device__ __forceinline__ SplitConsts split_consts()
+{
+    uint32_t m0 = 0x0000bf80u, m1 = 0xbf800000u;  // {-1, 0}, {0, -1}
+    asm volatile("" : "+s"(m0), "+s"(m1));
+    return SplitConsts{__builtin_bit_cast(bf16x2_t, m0), __builtin_bit_cast(bf16x2_t, m1)};
+}
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo,
+                                             const SplitConsts &k)
+{
+    hi = pack_bf16x2(a, b);
+    const bf16x2_t h = __builtin_bit_cast(bf16x2_t, hi);
+    lo = pack_bf16x2(__builtin_amdgcn_fdot2_f32_bf16(h, k.m0, a, false),
+                     __builtin_amdgcn_fdot2_f32_bf16(h, k.m1, b, false));
+}
+
 // DPP control words (GCN/CDNA encoding).
 constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]

@@ -114,6 +114,21 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
               lr = l & 15, lg = l >> 4;
     const int v0w = v0 + 16 * w;
 
+    // Every bf16 hi / lo split of the loop. With one wave per SIMD (NW == 4) a wave issues
+    // alone and each VALU instruction it saves counts: the dot-product residual, with gammaC
+    // S0 formed early (phase (a) below), saves 64 of ~330 a chunk (qk4_v8 batches of whole
+    // sequences 4-6 % faster on MI355X). With two waves per SIMD the 8-wave scan ran no
+    // faster with it (1-2 % slower with the early gammaC S0), so it keeps the plain split.
+    SplitConsts sk{};
+    if constexpr (NW == 4)
+        sk = split_consts();
+    auto split2 = [&](float a, float b, uint32_t &hi, uint32_t &lo) {
+        if constexpr (NW == 4)
+            split_bf16x2(a, b, hi, lo, sk);
+        else
+            split_bf16x2(a, b, hi, lo);
+    };
+
     // ---- copy plan. Every copy is a buffer load straight to LDS; per-lane source offsets
     // are chunk-invariant and computed once. Rows past a chunk's end fall outside the
     // chunk's buffer range and read as zero: those rows meet beta = 0 or the causal mask
@@ -318,10 +333,10 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-                split_bf16x2(S[2 * ks][0], S[2 * ks][1], h0, l0);
-                split_bf16x2(S[2 * ks][2], S[2 * ks][3], h1, l1);
-                split_bf16x2(S[2 * ks + 1][0], S[2 * ks + 1][1], h2, l2);
-                split_bf16x2(S[2 * ks + 1][2], S[2 * ks + 1][3], h3, l3);
+                split2(S[2 * ks][0], S[2 * ks][1], h0, l0);
+                split2(S[2 * ks][2], S[2 * ks][3], h1, l1);
+                split2(S[2 * ks + 1][0], S[2 * ks + 1][1], h2, l2);
+                split2(S[2 * ks + 1][2], S[2 * ks + 1][3], h3, l3);
                 Bh[ks] = u32x4{h0, h1, h2, h3};
                 Bl[ks] = u32x4{l0, l1, l2, l3};
             }
@@ -382,12 +397,24 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
         auto kA = [&](int s, int tt) {
             return *(const u32x4 *)(Kb + koffA[s] + 256 * (32 * (tt >> 1) + 4 * (tt & 1)));
         };
+        // NW == 4: S0's only other reader is (f), as gammaC S0. Scaled here (the asm keeps
+        // the product from being sunk into (f)), S0 dies in the split, whose dot-product
+        // residuals are then formed in S0's registers.
+        const float gC4 = NW == 4 ? *(const float *)(Gb + 768) : 0.f;
         auto split_s = [&](int s, u32x4 &bh, u32x4 &bl) {
+            const f32x4 s0 = S[2 * s], s1 = S[2 * s + 1];
+            if constexpr (NW == 4) {
+                S[2 * s] = gC4 * s0;
+                S[2 * s + 1] = gC4 * s1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    asm volatile("" : "+v"(S[2 * s][i]), "+v"(S[2 * s + 1][i]));
+            }
             uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-            split_bf16x2(S[2 * s][0], S[2 * s][1], h0, l0);
-            split_bf16x2(S[2 * s][2], S[2 * s][3], h1, l1);
-            split_bf16x2(S[2 * s + 1][0], S[2 * s + 1][1], h2, l2);
-            split_bf16x2(S[2 * s + 1][2], S[2 * s + 1][3], h3, l3);
+            split2(s0[0], s0[1], h0, l0);
+            split2(s0[2], s0[3], h1, l1);
+            split2(s1[0], s1[1], h2, l2);
+            split2(s1[2], s1[3], h3, l3);
             bh = u32x4{h0, h1, h2, h3};
             bl = u32x4{l0, l1, l2, l3};
         };
@@ -446,8 +473,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
             const float r2 = fmaf(-gm[tt][2], X[tt][2], bf16lo(vv[tt][1]));
             const float r3 = fmaf(-gm[tt][3], X[tt][3], bf16hi(vv[tt][1]));
             uint32_t h01, l01, h23, l23;
-            split_bf16x2(r0, r1, h01, l01);
-            split_bf16x2(r2, r3, h23, l23);
+            split2(r0, r1, h01, l01);
+            split2(r2, r3, h23, l23);
             const int e = 2 * (tt & 1);
             Rh[tt >> 1][e] = h01; Rh[tt >> 1][e + 1] = h23;
             Rl[tt >> 1][e] = l01; Rl[tt >> 1][e + 1] = l23;
@@ -499,8 +526,8 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
             uint32_t h01, l01, h23, l23;
-            split_bf16x2(dc[tt][0] * U[tt][0], dc[tt][1] * U[tt][1], h01, l01);
-            split_bf16x2(dc[tt][2] * U[tt][2], dc[tt][3] * U[tt][3], h23, l23);
+            split2(dc[tt][0] * U[tt][0], dc[tt][1] * U[tt][1], h01, l01);
+            split2(dc[tt][2] * U[tt][2], dc[tt][3] * U[tt][3], h23, l23);
             const uint32_t u01 = pack_bf16x2(U[tt][0], U[tt][1]), u23 = pack_bf16x2(U[tt][2], U[tt][3]);
             const int e = 2 * (tt & 1);
             Wh[tt >> 1][e] = h01; Wh[tt >> 1][e + 1] = h23;
@@ -566,7 +593,7 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
             __builtin_amdgcn_sched_barrier(0);
             if (gidx < 7)
                 ktRead(gidx + 1, kt[(gidx + 1) & 1]);
-            f32x4 acc = gC * S[gidx];
+            f32x4 acc = NW == 4 ? S[gidx] : gC * S[gidx];  // NW == 4: gammaC S0 from (a)
 #pragma unroll
             for (int sp = 0; sp < 2; ++sp) {
                 acc = mfma_bf16(kt[gidx & 1][sp], Wh[sp], acc);
@@ -638,10 +665,10 @@ __device__ __forceinline__ void scan_body(const ScanArgs &p, const ScanJob &job,
             const f32x4 a = *(const f32x4 *)(stg + 16 * j + 8 * c2);
             const f32x4 b = *(const f32x4 *)(stg + 16 * j + 8 * c2 + 4);
             uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
-            split_bf16x2(a[0], a[1], h0, l0);
-            split_bf16x2(a[2], a[3], h1, l1);
-            split_bf16x2(b[0], b[1], h2, l2);
-            split_bf16x2(b[2], b[3], h3, l3);
+            split2(a[0], a[1], h0, l0);
+            split2(a[2], a[3], h1, l1);
+            split2(b[0], b[1], h2, l2);
+            split2(b[2], b[3], h3, l3);
             const int un = 16 * j + ((cu0 + c2) ^ kswz(j));
             mt[un] = u32x4{h0, h1, h2, h3};
             mt[kMtUnits + un] = u32x4{l0, l1, l2, l3};
