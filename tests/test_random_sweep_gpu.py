@@ -1,7 +1,7 @@
 """Randomized parity sweep of gdn_prefill and gdn_decode against the float64 CPU oracle.
 
-Each case draws, from its own seed, a head layout (1-16 q/k heads, 1, 2 or 4 v-heads per
-q/k head), then for prefill a batch of 1-12 sequences whose lengths mix the chunk edges
+Each case draws, from its own seed, a head layout (1-16 q/k heads, 1-4 v-heads per q/k
+head), then for prefill a batch of 1-12 sequences whose lengths mix the chunk edges
 (0, 1, 63, 64, 65, 127, 128) with random lengths up to 4000 tokens, padding tokens that
 belong to no sequence, int32 or int64 cu_seqlens, a zero or random initial state and strong,
 mild or no decay; for decode a batch of 1-257 sequences. Bars as in the other parity tests
@@ -25,8 +25,8 @@ SEED0 = 7000
 
 
 def _layout(rnd):
-    hqk = rnd.choice([1, 2, 4, 8, 16])
-    return hqk, hqk * rnd.choice([1, 2, 4])
+    hqk = rnd.choice([1, 2, 3, 4, 8, 16])
+    return hqk, hqk * rnd.choice([1, 2, 3, 4])
 
 
 def _prefill_case(i):
